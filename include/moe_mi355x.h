@@ -1,0 +1,120 @@
+/*
+ * moe_mi355x.h -- C ABI of the MI355X (gfx950) rank-local FP8 MoE expert path.
+ *
+ * Every entry point takes raw device pointers, plain sizes and a HIP stream
+ * (passed as void*, a hipStream_t; NULL = the default stream), enqueues its
+ * kernels on that stream and returns immediately.  Nothing here allocates:
+ * the caller owns every buffer (the reference's ownership model, torch
+ * allocates and the ops write into caller buffers,
+ * moe_bench/overlap/overlap_forward.py:187-213).  Kernels keep no global state.
+ *
+ * Return value: 0 on success, a negative MOE_ERR_* code for an argument error
+ * (nothing is launched), MOE_ERR_LAUNCH if the HIP launch itself failed.
+ *
+ * Number formats: bf16 tensors are raw uint16 bit patterns; FP8 is OCP e4m3fn
+ * (one byte); scales are fp32.  Row-major everywhere.  Notation: T tokens,
+ * H hidden, I per-expert intermediate, E experts, k = top_k, S = T*k token
+ * slots (slot s = t*k + i), BM = block_size_m.
+ *
+ * Reference citations are to stmoonar/td_benchmark (paths under moe_bench/);
+ * the inner-op interfaces they replace are vLLM's as that code calls them.
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_ERR_NULL_POINTER (-1)
+#define MOE_ERR_BAD_SHAPE (-2)      /* negative size, dimension not a multiple of 128, misaligned pointer */
+#define MOE_ERR_BAD_BLOCK_SIZE (-3) /* block_size_m not in {16, 32, 64, 128} */
+#define MOE_ERR_CAPACITY (-4)       /* an output capacity is below what the shape needs */
+#define MOE_ERR_BAD_TOPK (-5)
+#define MOE_ERR_BAD_EXPERTS (-6)
+#define MOE_ERR_LAUNCH (-100)
+
+/* A1 / A7 -- dynamic 1x128 per-token-group FP8 activation quant.
+ * Replaces vLLM moe_kernel_quantize_input(A, None, float8_e4m3fn, False,
+ * [128,128]) as called at overlap/overlap_forward.py:257-259 and :282-284
+ * (arithmetic of verify.py:108-117).
+ * x [T,H] bf16 -> q [T,H] e4m3fn, scales [T, H/128] fp32; H % 128 == 0,
+ * x 16-byte aligned, q 8-byte aligned. */
+int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void* q_fp8, float* scales,
+                       void* stream);
+
+/* A2 -- 128x128 block FP8 weight quant (build time).
+ * Replaces quantize_block128 (data/checkpoint.py:28-40).
+ * w [E,N,K] fp32 -> q [E,N,K] e4m3fn, scales [E, ceil(N/128), ceil(K/128)]. */
+int moe_quant_block128(const float* w, int64_t E, int64_t N, int64_t K, void* q_fp8,
+                       float* scales, void* stream);
+
+/* A3 -- moe_align_block_size.
+ * Replaces vLLM moe_align_block_size(topk_ids, BM, E, None) as called at
+ * overlap/overlap_forward.py:165-169 and schemes/shared_expert.py:61-62.
+ * topk_ids [S] int32 (flattened [T,k]) -> sorted_ids [max_padded] int32,
+ * expert_ids [ceil(max_padded/BM)] int32, ntpp [1] int32.  Canonical stable
+ * order inside each expert; pad value S; expert_ids -1 past ntpp.  Ids outside
+ * [0,E) are dropped.  E <= 1024.  max_padded >= moe_align_max_padded(S,E,BM);
+ * workspace >= moe_align_workspace_bytes(S,E) bytes of device memory. */
+int64_t moe_align_max_padded(int64_t S, int32_t E, int32_t block_size_m);
+int64_t moe_align_workspace_bytes(int64_t S, int32_t E);
+int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t block_size_m,
+                         int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
+                         int64_t max_padded, void* workspace, void* stream);
+
+/* A5 / A8 -- block-scaled FP8 grouped GEMM, plain bf16 epilogue.
+ * Replaces vLLM dispatch_fused_moe_kernel(A, B, C, A_scale, B_scale, None,
+ * topk_weights, sorted_token_ids, expert_ids, num_tokens_post_padded,
+ * mul_routed_weight, top_k, config, compute_type=bf16, use_fp8_w8a8=True,
+ * block_shape=[128,128]) as called at overlap/kernels.py:288-310 and
+ * schemes/shared_expert.py:102-123; semantics of overlap/kernels.py:95-214.
+ * C[s, n] = bf16( w[s]? * sum_kb dot(A[row,kb], B[e,n,kb]) * A_scale[row,kb] * B_scale[e,n/128,kb] )
+ * for every placed slot s, row = a_by_pos ? (sorted position) : s / top_k.
+ * topk_weights NULL = mul_routed_weight False.  A [rows,K], A_scale [rows,K/128],
+ * B [E,N,K], B_scale [E,N/128,K/128], C [S,N] bf16.  N, K % 128 == 0. */
+int moe_grouped_gemm(const void* A, const float* A_scale, const void* B, const float* B_scale,
+                     const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                     const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
+                     int64_t N, int64_t K, int32_t E, int32_t block_size_m, int64_t max_padded,
+                     void* C, void* stream);
+
+/* A5 + A6 + A7 fused -- W13 grouped GEMM with SiLU*up and 1x128 FP8 quant of
+ * the intermediate in the epilogue.
+ * Replaces the sequence dispatch_fused_moe_kernel(W13, mul_routed_weight=False,
+ * top_k=k) -> torch.ops._C.silu_and_mul -> moe_kernel_quantize_input
+ * (overlap/overlap_forward.py:261-284).  Outputs are indexed by sorted
+ * position p (not by slot): hq [max_padded, I] e4m3fn, hs [max_padded, I/128]
+ * fp32, so the W2 GEMM reads them with a_by_pos = 1.
+ * Aq [T,H], A_scale [T,H/128], W13 [E,2I,H] (gate rows [0,I), up rows [I,2I),
+ * verify.py:36), W13_scale [E,2I/128,H/128].  H, I % 128 == 0. */
+int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,
+                            const float* W13_scale, const int32_t* sorted_ids,
+                            const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                            int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
+                            int64_t max_padded, void* hq, float* hs, void* stream);
+
+/* A6 -- silu_and_mul.  Replaces torch.ops._C.silu_and_mul(out, in)
+ * (overlap/overlap_forward.py:277-279): h[r,j] = bf16(silu(c[r,j]) * c[r,I+j]).
+ * c [R, 2I] bf16 -> h [R, I] bf16; I % 8 == 0. */
+int moe_silu_and_mul(const void* c_bf16, int64_t R, int64_t I, void* h_bf16, void* stream);
+
+/* A9 -- top-k un-permute / reduce.  Replaces torch.sum(C_down.view(T,k,H),
+ * dim=1) (overlap/overlap_forward.py:304-313): y[t] = bf16(sum_i D[t*k+i]),
+ * fp32 accumulation.  D [T*k, H] bf16 -> y [T, H] bf16; H % 8 == 0, k <= 32. */
+int moe_reduce_topk(const void* D_bf16, int64_t T, int32_t top_k, int64_t H, void* y_bf16,
+                    void* stream);
+
+/* Test hook (no reference counterpart): one 16x16x128 FP8 MFMA through the
+ * GEMM's own LDS swizzle, fragment loader and output mapping.
+ * A [16,128], B [16,128] e4m3fn -> C [16,16] fp32 = A . B^T. */
+int moe_debug_mfma_probe(const void* A, const void* B, float* C, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

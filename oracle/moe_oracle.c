@@ -1,0 +1,297 @@
+/*
+ * CPU oracle for the rank-local FP8 MoE expert path.  TEST INFRASTRUCTURE ONLY:
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may call it,
+ * as the checker; nothing in the product path links or calls it.
+ *
+ * Each function restates the reference's arithmetic, read as text, and cites
+ * the reference file:line it follows (paths relative to the reference root,
+ * moe_bench/ unless said otherwise).  The reference itself is Python over
+ * torch and vLLM; vLLM is not vendored, so the vLLM stages are restated from
+ * the reference's in-repo decomposition (overlap/overlap_forward.py) and its
+ * in-repo copy of the grouped-GEMM kernel (overlap/kernels.py).
+ *
+ * Pinning (what independent checks each function is held to) is listed in
+ * oracle/README.md and exercised by tests/test_oracle_*.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define FP8_MAX 448.0f
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---------------------------------------------------------------------------
+ * Scalar conversions.
+ * ------------------------------------------------------------------------- */
+
+/* fp32 -> OCP e4m3fn, round-to-nearest-even, with torch's out-of-range rule:
+ * |x| >= 480 (and NaN/inf) becomes the NaN code 0x7F|sign, 464 < |x| < 480
+ * rounds up into 0x7F.  This is what `tensor.to(torch.float8_e4m3fn)` does in
+ * verify.py:116 and data/checkpoint.py:168; callers clamp to +-448 first, so
+ * only [-448, 448] reaches it on the path. */
+uint8_t oracle_f32_to_e4m3(float f) {
+    uint32_t u = f2u(f);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+    u &= 0x7FFFFFFFu;
+    if (u >= 0x43F00000u) return sign | 0x7F;          /* >= 480, inf, NaN */
+    if (u < 0x3C800000u) {                              /* < 2^-6: subnormal */
+        float a = u2f(u) * 512.0f;                      /* exact: times 2^9 */
+        float fl = floorf(a), frac = a - fl;             /* both exact (a<8) */
+        int r = (int)fl;
+        if (frac > 0.5f || (frac == 0.5f && (r & 1))) r += 1;  /* RNE */
+        return sign | (uint8_t)r;                        /* r == 8 -> 2^-6   */
+    }
+    uint32_t exp = (u >> 23) - 127 + 7;                  /* 1..15 */
+    uint32_t mant = u & 0x7FFFFFu;
+    uint32_t r = (exp << 3) | (mant >> 20);
+    uint32_t rem = mant & 0xFFFFFu;
+    if (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) r += 1;
+    return sign | (uint8_t)r;
+}
+
+void oracle_f32_to_e4m3_array(const float* x, int64_t n, uint8_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_e4m3(x[i]);
+}
+
+/* OCP e4m3fn -> fp32 (exact). */
+float oracle_e4m3_to_f32(uint8_t c) {
+    int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else v = ldexpf(1.0f + m / 8.0f, e - 7);
+    return s ? -v : v;
+}
+
+/* fp32 -> bf16 bits, round-to-nearest-even (torch's `.to(torch.bfloat16)`
+ * for finite values). */
+uint16_t oracle_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t b) { return u2f(((uint32_t)b) << 16); }
+
+static inline float bf16r(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16(f)); }
+
+/* ---------------------------------------------------------------------------
+ * A1 / A7: dynamic 1x128 per-token-group activation quant.
+ * Follows verify.py:108-117 (_group_quant_dequant) for the arithmetic:
+ *   scale = max(amax / 448, 1e-12)      (fp32 division, verify.py:115)
+ *   q     = e4m3(clamp(x / scale, +-448)) (fp32 division, verify.py:116)
+ * and overlap/overlap_forward.py:257-259 for the output form: codes [T,H]
+ * plus row-major scales [T, ceil(H/128)] (indexed [token, kblk] by the GEMM,
+ * overlap/kernels.py:141,175-177).  Ragged H is zero-padded (verify.py:112).
+ * x is bf16 bits.
+ * ------------------------------------------------------------------------- */
+void oracle_quant_group128(const uint16_t* x, int64_t T, int64_t H,
+                           uint8_t* q, float* s) {
+    int64_t G = (H + 127) / 128;
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t g = 0; g < G; ++g) {
+            int64_t k0 = g * 128, k1 = k0 + 128 < H ? k0 + 128 : H;
+            float amax = 0.0f;
+            for (int64_t k = k0; k < k1; ++k) {
+                float v = fabsf(oracle_bf16_to_f32(x[t * H + k]));
+                if (v > amax) amax = v;
+            }
+            float sc = amax / FP8_MAX;
+            if (sc < 1e-12f) sc = 1e-12f;
+            s[t * G + g] = sc;
+            for (int64_t k = k0; k < k1; ++k) {
+                float v = oracle_bf16_to_f32(x[t * H + k]) / sc;
+                if (v > FP8_MAX) v = FP8_MAX;
+                if (v < -FP8_MAX) v = -FP8_MAX;
+                q[t * H + k] = oracle_f32_to_e4m3(v);
+            }
+        }
+    }
+}
+
+/* Same quant over fp32 input (used by the golden's quant-dequant of the fp32
+ * intermediate, verify.py:38, where x is already fp32). Writes the
+ * dequantised values back (quant(x) * scale), verify.py:116. */
+void oracle_group_quant_dequant_f32(const float* x, int64_t R, int64_t H, float* out) {
+    for (int64_t r = 0; r < R; ++r) {
+        for (int64_t k0 = 0; k0 < H; k0 += 128) {
+            int64_t k1 = k0 + 128 < H ? k0 + 128 : H;
+            float amax = 0.0f;
+            for (int64_t k = k0; k < k1; ++k) {
+                float v = fabsf(x[r * H + k]);
+                if (v > amax) amax = v;
+            }
+            float sc = amax / FP8_MAX;
+            if (sc < 1e-12f) sc = 1e-12f;
+            for (int64_t k = k0; k < k1; ++k) {
+                float v = x[r * H + k] / sc;
+                if (v > FP8_MAX) v = FP8_MAX;
+                if (v < -FP8_MAX) v = -FP8_MAX;
+                out[r * H + k] = oracle_e4m3_to_f32(oracle_f32_to_e4m3(v)) * sc;
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------
+ * A2: 128x128 weight block quant, data/checkpoint.py:28-40 (loop form of
+ * tests/test_quantize.py:9-24).  w fp32 [E,N,K] -> q [E,N,K], s [E,nb,kb].
+ * ------------------------------------------------------------------------- */
+void oracle_quant_block128(const float* w, int64_t E, int64_t N, int64_t K,
+                           uint8_t* q, float* s) {
+    int64_t NB = (N + 127) / 128, KB = (K + 127) / 128;
+    for (int64_t e = 0; e < E; ++e)
+        for (int64_t nb = 0; nb < NB; ++nb)
+            for (int64_t kb = 0; kb < KB; ++kb) {
+                int64_t n0 = nb * 128, n1 = n0 + 128 < N ? n0 + 128 : N;
+                int64_t k0 = kb * 128, k1 = k0 + 128 < K ? k0 + 128 : K;
+                float amax = 0.0f;
+                for (int64_t n = n0; n < n1; ++n)
+                    for (int64_t k = k0; k < k1; ++k) {
+                        float v = fabsf(w[(e * N + n) * K + k]);
+                        if (v > amax) amax = v;
+                    }
+                float sc = amax / FP8_MAX;
+                if (sc < 1e-12f) sc = 1e-12f;
+                s[(e * NB + nb) * KB + kb] = sc;
+                for (int64_t n = n0; n < n1; ++n)
+                    for (int64_t k = k0; k < k1; ++k) {
+                        float v = w[(e * N + n) * K + k] / sc;
+                        if (v > FP8_MAX) v = FP8_MAX;
+                        if (v < -FP8_MAX) v = -FP8_MAX;
+                        q[(e * N + n) * K + k] = oracle_f32_to_e4m3(v);
+                    }
+            }
+}
+
+/* A2 dequant to bf16 bits, data/checkpoint.py:43-52: bf16(fp8 * scale). */
+void oracle_dequant_block128(const uint8_t* q, const float* s, int64_t E, int64_t N,
+                             int64_t K, uint16_t* out) {
+    int64_t NB = (N + 127) / 128, KB = (K + 127) / 128;
+    for (int64_t e = 0; e < E; ++e)
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t k = 0; k < K; ++k) {
+                float sc = s[(e * NB + n / 128) * KB + k / 128];
+                out[(e * N + n) * K + k] =
+                    oracle_f32_to_bf16(oracle_e4m3_to_f32(q[(e * N + n) * K + k]) * sc);
+            }
+}
+
+/* ---------------------------------------------------------------------------
+ * A3: moe_align_block_size.  Closed form (the padded-cumsum of
+ * tdx/kernels/moe_utils.py:168-217 with vLLM's sizing and pad value, call
+ * sites overlap/overlap_forward.py:165-169):
+ *   c_e = #slots routed to e; p_e = ceil(c_e/BM)*BM; off_e = sum_{e'<e} p_e'
+ *   sorted[off_e + j] = j-th slot (flat t*k+i, ascending) routed to e
+ *   pad value = S (token_mask = id < num_valid_tokens, overlap/kernels.py:108-110)
+ *   expert_ids[b] = e for blocks of e, -1 beyond ntpp; ntpp = sum p_e.
+ * Experts outside [0,E) (an expert_map's -1) are not placed.
+ * Returns 0, or -1 if max_padded is too small.
+ * ------------------------------------------------------------------------- */
+int oracle_moe_align(const int32_t* ids, int64_t S, int32_t E, int32_t BM,
+                     int32_t* sorted, int32_t* expert_ids, int32_t* ntpp,
+                     int64_t max_padded) {
+    int64_t* cnt = (int64_t*)calloc((size_t)E, sizeof(int64_t));
+    int64_t* off = (int64_t*)calloc((size_t)E + 1, sizeof(int64_t));
+    for (int64_t s = 0; s < S; ++s)
+        if (ids[s] >= 0 && ids[s] < E) cnt[ids[s]]++;
+    for (int32_t e = 0; e < E; ++e)
+        off[e + 1] = off[e] + (cnt[e] + BM - 1) / BM * BM;
+    int64_t total = off[E];
+    if (total > max_padded) { free(cnt); free(off); return -1; }
+    for (int64_t p = 0; p < max_padded; ++p) sorted[p] = (int32_t)S;
+    int64_t max_blocks = (max_padded + BM - 1) / BM;
+    for (int64_t b = 0; b < max_blocks; ++b) expert_ids[b] = -1;
+    for (int32_t e = 0; e < E; ++e)
+        for (int64_t b = off[e] / BM; b < off[e + 1] / BM; ++b) expert_ids[b] = e;
+    int64_t* fill = (int64_t*)calloc((size_t)E, sizeof(int64_t));
+    for (int64_t s = 0; s < S; ++s) {
+        int32_t e = ids[s];
+        if (e < 0 || e >= E) continue;
+        sorted[off[e] + fill[e]++] = (int32_t)s;
+    }
+    *ntpp = (int32_t)total;
+    free(cnt); free(off); free(fill);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------
+ * A5 / A8: block-scaled FP8 grouped GEMM, overlap/kernels.py:95-214.
+ * For every block b < ntpp/BM with expert e = expert_ids[b] (skip e == -1,
+ * kernels.py:112-120), every position p in the block whose slot
+ * s = sorted[p] < S (token mask, kernels.py:108-110):
+ *   row   = a_row_by_pos ? p : s / top_k        (kernels.py:124-126)
+ *   acc_n = sum_kb ( sum_{k in kb} A[row,k] * B[e,n,k] ) * a_s[row,kb] * b_s[e,n/128,kb]
+ *           (kernels.py:172-179, evaluated left to right in fp32 as there;
+ *            the inner dot is formed exactly in double and rounded once)
+ *   if mul_routed_weight: acc_n *= topk_w[s]     (kernels.py:192-194)
+ *   out[s, n] = bf16(acc_n)                       (kernels.py:198-210)
+ * A: fp8 codes [rows, K]; a_s [rows, ceil(K/128)]; B: [E, N, K]; b_s
+ * [E, ceil(N/128), ceil(K/128)].  out: bf16 bits [S, N] (rows by slot).
+ * ------------------------------------------------------------------------- */
+void oracle_grouped_gemm(const uint8_t* A, const float* a_s, const uint8_t* B,
+                         const float* b_s, const int32_t* sorted,
+                         const int32_t* expert_ids, int32_t ntpp, int32_t BM,
+                         int64_t S, int32_t top_k, int64_t N, int64_t K,
+                         int32_t a_row_by_pos, const float* topk_w,
+                         uint16_t* out) {
+    int64_t KB = (K + 127) / 128, NB = (N + 127) / 128;
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = oracle_e4m3_to_f32((uint8_t)i);
+    for (int64_t p = 0; p < ntpp; ++p) {
+        int32_t e = expert_ids[p / BM];
+        int64_t s = sorted[p];
+        if (e < 0 || s >= S) continue;
+        int64_t row = a_row_by_pos ? p : s / top_k;
+        const uint8_t* a = A + row * K;
+        for (int64_t n = 0; n < N; ++n) {
+            const uint8_t* w = B + ((int64_t)e * N + n) * K;
+            float acc = 0.0f;
+            for (int64_t kb = 0; kb < KB; ++kb) {
+                double dot = 0.0;
+                int64_t k1 = (kb + 1) * 128 < K ? (kb + 1) * 128 : K;
+                for (int64_t k = kb * 128; k < k1; ++k)
+                    dot += (double)lut[a[k]] * (double)lut[w[k]];
+                float t = (float)dot * a_s[row * KB + kb];
+                t = t * b_s[((int64_t)e * NB + n / 128) * KB + kb];
+                acc = acc + t;
+            }
+            if (topk_w) acc = acc * topk_w[s];
+            out[s * N + n] = oracle_f32_to_bf16(acc);
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------
+ * A6: silu_and_mul, overlap/overlap_forward.py:277-279 with the golden's
+ * split (gate = first I columns, up = last I, verify.py:36-37):
+ *   h[r, j] = bf16( silu(float(c[r, j])) * float(c[r, I + j]) ),
+ *   silu(x) = x / (1 + exp(-x)) in fp32.   c, h: bf16 bits.
+ * ------------------------------------------------------------------------- */
+void oracle_silu_and_mul(const uint16_t* c, int64_t R, int64_t I, uint16_t* h) {
+    for (int64_t r = 0; r < R; ++r)
+        for (int64_t j = 0; j < I; ++j) {
+            float g = oracle_bf16_to_f32(c[r * 2 * I + j]);
+            float u = oracle_bf16_to_f32(c[r * 2 * I + I + j]);
+            float sg = g / (1.0f + expf(-g));
+            h[r * I + j] = oracle_f32_to_bf16(sg * u);
+        }
+}
+
+/* ---------------------------------------------------------------------------
+ * A9: top-k un-permute / reduce, overlap/overlap_forward.py:304-313:
+ *   y[t, :] = bf16( sum_i float(D[t*k + i, :]) )   (fp32, i ascending).
+ * ------------------------------------------------------------------------- */
+void oracle_moe_reduce(const uint16_t* D, int64_t T, int32_t k, int64_t H, uint16_t* y) {
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t n = 0; n < H; ++n) {
+            float acc = 0.0f;
+            for (int32_t i = 0; i < k; ++i)
+                acc += oracle_bf16_to_f32(D[(t * k + i) * H + n]);
+            y[t * H + n] = oracle_f32_to_bf16(acc);
+        }
+}

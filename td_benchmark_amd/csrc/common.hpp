@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 MoE expert path.
+//
+// Number formats: activations and outputs are bf16 (raw uint16 bits), FP8 is
+// OCP e4m3fn (the format gfx950's conversion and MFMA f8f6f4 instructions use
+// with format code 0), scales are fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_mi355x.h"
+
+#define MOE_HOST_DEVICE __host__ __device__ __forceinline__
+#define MOE_DEVICE __device__ __forceinline__
+
+namespace moe {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kScaleFloor = 1e-12f;   // verify.py:115 clamp(min=1e-12)
+
+// Status codes returned by every extern "C" entry point.
+enum Status : int {
+  kOk = 0,
+  kErrNullPointer = -1,
+  kErrBadShape = -2,        // a size is negative, or a dimension is not a multiple of 128
+  kErrBadBlockSize = -3,    // block_size_m not in {16, 32, 64, 128}
+  kErrCapacity = -4,        // an output buffer is smaller than the shape needs
+  kErrBadTopK = -5,
+  kErrBadExperts = -6,
+  kErrLaunch = -100,        // hipGetLastError() reported a launch failure
+};
+static_assert(kErrNullPointer == MOE_ERR_NULL_POINTER && kErrBadShape == MOE_ERR_BAD_SHAPE &&
+                  kErrBadBlockSize == MOE_ERR_BAD_BLOCK_SIZE && kErrCapacity == MOE_ERR_CAPACITY &&
+                  kErrBadTopK == MOE_ERR_BAD_TOPK && kErrBadExperts == MOE_ERR_BAD_EXPERTS &&
+                  kErrLaunch == MOE_ERR_LAUNCH,
+              "status codes must match the C header");
+
+MOE_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// fp32 -> bf16, round to nearest even (finite values; NaN stays NaN).
+MOE_DEVICE uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+MOE_DEVICE float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+
+// Correctly rounded x / s given inv = RN(1/s): q0 = RN(x*inv); the residual
+// x - q0*s is exact under fma; one correction step gives RN(x/s) (Markstein's
+// final-step theorem for round-to-nearest, valid away from overflow and
+// subnormal quotients; see the quant tests for the exhaustive CPU check).
+MOE_DEVICE float div_by(float x, float s, float inv) {
+  float q0 = x * inv;
+  float r = __builtin_fmaf(-q0, s, x);
+  return __builtin_fmaf(r, inv, q0);
+}
+
+MOE_DEVICE float clamp_fp8(float v) { return __builtin_amdgcn_fmed3f(v, -kFp8Max, kFp8Max); }
+
+// Four fp32 (already clamped to +-448) -> four packed e4m3fn bytes, RNE.
+MOE_DEVICE uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// Group scale of verify.py:115: max(amax / 448, 1e-12), IEEE division.
+MOE_DEVICE float group_scale(float amax) {
+  float s = amax / kFp8Max;
+  return s < kScaleFloor ? kScaleFloor : s;
+}
+
+}  // namespace moe

@@ -1,0 +1,110 @@
+// A9: top-k un-permute / reduce, and A6 as a standalone op.
+//
+// moe_reduce_topk: y[t, :] = bf16( sum_{i<k} float(D[t*k + i, :]) ), fp32
+// accumulation in ascending i -- the reference's
+// torch.sum(C_down.view(T, k, H), dim=1) (overlap/overlap_forward.py:304-313);
+// the routed weights were already applied by the W2 GEMM epilogue.
+// HBM-bound: 2*k*H bytes read + 2*H written per token; each thread owns 16 B
+// (8 columns) of one token and keeps its k row loads in flight together.
+//
+// moe_silu_and_mul: h[r, j] = bf16( silu(c[r, j]) * c[r, I + j] ) with fp32
+// math (torch.ops._C.silu_and_mul, overlap/overlap_forward.py:277-279).  The
+// fused W13 kernel performs the same arithmetic in its epilogue; this op
+// serves the unfused chain.
+#include "common.hpp"
+
+namespace moe {
+
+constexpr int kMaxTopK = 32;
+
+template <int KMAX>
+__global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __restrict__ D,
+                                                          uint16_t* __restrict__ y, int64_t T,
+                                                          int k, int64_t chunks_per_row) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= T * chunks_per_row) return;
+  const int64_t t = idx / chunks_per_row;
+  const int64_t cc = idx % chunks_per_row;
+  const int64_t H = chunks_per_row * 8;
+  v4i rows[KMAX];
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i)
+    if (i < k) rows[i] = *reinterpret_cast<const v4i*>(D + (t * k + i) * H + cc * 8);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    if (i < k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = (uint32_t)rows[i][j];
+        acc[2 * j] += __uint_as_float(w << 16);
+        acc[2 * j + 1] += __uint_as_float(w & 0xFFFF0000u);
+      }
+    }
+  }
+  v4i out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    out[j] = (int)(f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16));
+  *reinterpret_cast<v4i*>(y + t * H + cc * 8) = out;
+}
+
+__global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __restrict__ c,
+                                                           uint16_t* __restrict__ h, int64_t R,
+                                                           int64_t I) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t chunks = I / 8;
+  if (idx >= R * chunks) return;
+  const int64_t r = idx / chunks, cc = idx % chunks;
+  const v4i gv = *reinterpret_cast<const v4i*>(c + r * 2 * I + cc * 8);
+  const v4i uv = *reinterpret_cast<const v4i*>(c + r * 2 * I + I + cc * 8);
+  v4i out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t gw = (uint32_t)gv[j], uw = (uint32_t)uv[j];
+    const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xFFFF0000u);
+    const float u0 = __uint_as_float(uw << 16), u1 = __uint_as_float(uw & 0xFFFF0000u);
+    const float h0 = g0 / (1.0f + __expf(-g0)) * u0;
+    const float h1 = g1 / (1.0f + __expf(-g1)) * u1;
+    out[j] = (int)(f32_to_bf16_bits(h0) | (f32_to_bf16_bits(h1) << 16));
+  }
+  *reinterpret_cast<v4i*>(h + r * I + cc * 8) = out;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_reduce_topk(const void* D_bf16, int64_t T, int32_t top_k, int64_t H, void* y,
+                               void* stream) {
+  if (T < 0 || H < 0) return kErrBadShape;
+  if (top_k <= 0 || top_k > kMaxTopK) return kErrBadTopK;
+  if (T == 0 || H == 0) return kOk;
+  if (!D_bf16 || !y) return kErrNullPointer;
+  if (H % 8 != 0 || !aligned16(D_bf16) || !aligned16(y)) return kErrBadShape;
+  const int64_t cpr = H / 8;
+  const int64_t blocks = (T * cpr + 255) / 256;
+  hipStream_t st = (hipStream_t)stream;
+  if (top_k <= 8) {
+    hipLaunchKernelGGL(reduce_topk_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const uint16_t*)D_bf16, (uint16_t*)y, T, (int)top_k, cpr);
+  } else {
+    hipLaunchKernelGGL(reduce_topk_kernel<kMaxTopK>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const uint16_t*)D_bf16, (uint16_t*)y, T, (int)top_k, cpr);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_silu_and_mul(const void* c_bf16, int64_t R, int64_t I, void* h_bf16,
+                                void* stream) {
+  if (R < 0 || I < 0) return kErrBadShape;
+  if (R == 0 || I == 0) return kOk;
+  if (!c_bf16 || !h_bf16) return kErrNullPointer;
+  if (I % 8 != 0 || !aligned16(c_bf16) || !aligned16(h_bf16)) return kErrBadShape;
+  const int64_t blocks = (R * (I / 8) + 255) / 256;
+  hipLaunchKernelGGL(silu_and_mul_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)c_bf16, (uint16_t*)h_bf16, R, I);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}

@@ -1,0 +1,145 @@
+// A1 / A7: dynamic 1x128 per-token-group FP8 quant of bf16 activations.
+// A2:      128x128 block FP8 quant of fp32 weights (build time).
+//
+// Arithmetic follows reference moe_bench/verify.py:108-117 and
+// data/checkpoint.py:28-40: scale = max(amax/448, 1e-12) by IEEE division,
+// code = e4m3fn_RNE(clamp(x / scale, +-448)).
+//
+// quant_group128 is HBM-bound: 2 B in + 1 B out per element + 4 B of scale per
+// 128 elements.  Sixteen lanes own one 128-element group (16 B = 8 bf16 each),
+// so every wave reads 1 KiB and writes 512 B contiguously with 128-bit loads;
+// the group amax is a 16-lane xor-shuffle reduction; each thread keeps four
+// independent groups in flight to cover HBM latency.
+#include "common.hpp"
+
+namespace moe {
+
+constexpr int kQuantThreads = 256;
+constexpr int kQuantUnroll = 4;  // chunks (16 B) per thread
+constexpr int kQuantChunksPerBlock = kQuantThreads * kQuantUnroll;
+
+__global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ s,
+    int64_t n_chunks) {
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kQuantChunksPerBlock;
+  v4i raw[kQuantUnroll];
+#pragma unroll
+  for (int i = 0; i < kQuantUnroll; ++i) {
+    int64_t ch = base + tid + i * kQuantThreads;
+    if (ch < n_chunks) {
+      raw[i] = *reinterpret_cast<const v4i*>(x + ch * 8);
+    } else {
+      raw[i] = (v4i){0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kQuantUnroll; ++i) {
+    int64_t ch = base + tid + i * kQuantThreads;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = (uint32_t)raw[i][j];
+      v[2 * j] = __uint_as_float(w << 16);
+      v[2 * j + 1] = __uint_as_float(w & 0xFFFF0000u);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    // 16 lanes of one group are 16 consecutive lanes of the wave.
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    float sc = group_scale(amax);
+    float inv = 1.0f / sc;
+    uint32_t lo = pack4_e4m3(clamp_fp8(div_by(v[0], sc, inv)), clamp_fp8(div_by(v[1], sc, inv)),
+                             clamp_fp8(div_by(v[2], sc, inv)), clamp_fp8(div_by(v[3], sc, inv)));
+    uint32_t hi = pack4_e4m3(clamp_fp8(div_by(v[4], sc, inv)), clamp_fp8(div_by(v[5], sc, inv)),
+                             clamp_fp8(div_by(v[6], sc, inv)), clamp_fp8(div_by(v[7], sc, inv)));
+    if (ch < n_chunks) {
+      *reinterpret_cast<uint2*>(q + ch * 8) = make_uint2(lo, hi);
+      if ((tid & 15) == 0) s[ch >> 4] = sc;
+    }
+  }
+}
+
+// One workgroup per 128x128 block of one expert.  w fp32 [E, N, K] row-major.
+__global__ __launch_bounds__(256) void quant_block128_kernel(
+    const float* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ s,
+    int64_t N, int64_t K, int64_t NB, int64_t KB) {
+  const int64_t blk = blockIdx.x;
+  const int64_t kb = blk % KB;
+  const int64_t nb = (blk / KB) % NB;
+  const int64_t e = blk / (KB * NB);
+  const int tid = threadIdx.x;
+  const int col = (tid & 31) * 4;          // 32 threads x 4 columns = 128
+  const int row0 = tid >> 5;               // 8 rows per pass, 16 passes
+  const int64_t k = kb * 128 + col;
+  float vals[16][4];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    int64_t n = nb * 128 + row0 + p * 8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = 0.0f;
+      if (n < N && k + j < K) v = w[(e * N + n) * K + k + j];
+      vals[p][j] = v;
+      amax = fmaxf(amax, fabsf(v));
+    }
+  }
+  __shared__ float red[8];
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sc = group_scale(amax);
+  if (tid == 0) s[(e * NB + nb) * KB + kb] = sc;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    int64_t n = nb * 128 + row0 + p * 8;
+    if (n >= N) continue;
+    float a = clamp_fp8(vals[p][0] / sc), b = clamp_fp8(vals[p][1] / sc);
+    float c = clamp_fp8(vals[p][2] / sc), d = clamp_fp8(vals[p][3] / sc);
+    uint32_t packed = pack4_e4m3(a, b, c, d);
+    uint8_t* dst = q + (e * N + n) * K + k;
+    if (k + 3 < K && ((K & 3) == 0)) {
+      *reinterpret_cast<uint32_t*>(dst) = packed;
+    } else {
+      for (int j = 0; j < 4; ++j)
+        if (k + j < K) dst[j] = (uint8_t)(packed >> (8 * j));
+    }
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void* q_fp8,
+                                  float* scales, void* stream) {
+  if (T < 0 || H < 0) return kErrBadShape;
+  if (T == 0 || H == 0) return kOk;
+  if (!x_bf16 || !q_fp8 || !scales) return kErrNullPointer;
+  if (H % 128 != 0) return kErrBadShape;
+  if (((uintptr_t)x_bf16 & 15) != 0 || ((uintptr_t)q_fp8 & 7) != 0) return kErrBadShape;
+  const int64_t n_chunks = T * H / 8;
+  const int64_t blocks = (n_chunks + kQuantChunksPerBlock - 1) / kQuantChunksPerBlock;
+  hipLaunchKernelGGL(quant_group128_kernel, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, (uint8_t*)q_fp8, scales,
+                     n_chunks);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_quant_block128(const float* w, int64_t E, int64_t N, int64_t K, void* q_fp8,
+                                  float* scales, void* stream) {
+  if (E < 0 || N < 0 || K < 0) return kErrBadShape;
+  if (E == 0 || N == 0 || K == 0) return kOk;
+  if (!w || !q_fp8 || !scales) return kErrNullPointer;
+  const int64_t NB = (N + 127) / 128, KB = (K + 127) / 128;
+  hipLaunchKernelGGL(quant_block128_kernel, dim3((unsigned)(E * NB * KB)), dim3(256), 0,
+                     (hipStream_t)stream, w, (uint8_t*)q_fp8, scales, N, K, NB, KB);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}

@@ -1,0 +1,341 @@
+"""Torch-facing operators of the MI355X MoE expert path.
+
+Each function mirrors the vLLM operator the reference calls at that point of
+its ``fused_experts`` decomposition (moe_bench/overlap/overlap_forward.py:
+153-313), with the same argument meaning, and launches the hand-written HIP
+kernels of ``libmoe_mi355x.so`` through the C ABI (include/moe_mi355x.h) on the
+current torch stream.  PyTorch only provides device memory and the stream;
+there is no torch compute and no fallback on the path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any
+
+import torch
+
+from ._lib import check, lib
+
+FP8 = torch.float8_e4m3fn
+BLOCK_SHAPE = [128, 128]
+SUPPORTED_BLOCK_M = (16, 32, 64, 128)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream: torch.cuda.Stream | None = None) -> ctypes.c_void_p:
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+# ---------------------------------------------------------------------------
+# A1 / A7 -- 1x128 activation quant
+# ---------------------------------------------------------------------------
+
+def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128,
+                              out_q: torch.Tensor | None = None,
+                              out_s: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [T,H] bf16 -> (q [T,H] e4m3fn, scales [T,H/128] fp32).
+
+    Arithmetic of moe_bench/verify.py:108-117 (scale = max(amax/448, 1e-12),
+    q = e4m3(clamp(x/scale, +-448))); output form of vLLM's
+    per_token_group_quant_fp8 as consumed by the grouped GEMM."""
+    if group_size != 128:
+        raise NotImplementedError("only 1x128 activation groups are implemented")
+    _need(x, "x", torch.bfloat16)
+    T, H = x.shape
+    q = torch.empty((T, H), dtype=FP8, device=x.device) if out_q is None else out_q
+    s = torch.empty((T, H // 128), dtype=torch.float32, device=x.device) if out_s is None else out_s
+    check(lib().moe_quant_group128(_ptr(x), T, H, _ptr(q), _ptr(s), _stream()), "moe_quant_group128")
+    return q, s
+
+
+def moe_kernel_quantize_input(A: torch.Tensor, A_scale: torch.Tensor | None, quant_dtype: Any,
+                              per_act_token_quant: bool, block_shape: list[int] | None = None):
+    """Signature of vLLM's moe_kernel_quantize_input as the reference calls it
+    (overlap/overlap_forward.py:257-259): only the dynamic FP8 1x128 form."""
+    if A_scale is not None or quant_dtype != FP8 or per_act_token_quant or list(block_shape or []) != BLOCK_SHAPE:
+        raise NotImplementedError("only dynamic float8_e4m3fn with block_shape [128,128] is implemented")
+    return per_token_group_quant_fp8(A)
+
+
+# ---------------------------------------------------------------------------
+# A2 -- 128x128 weight quant (build time)
+# ---------------------------------------------------------------------------
+
+def quantize_block128(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 [E,N,K] -> (e4m3fn [E,N,K], scales [E,ceil(N/128),ceil(K/128)]),
+    moe_bench/data/checkpoint.py:28-40 on the GPU."""
+    _need(w, "w", torch.float32)
+    E, N, K = w.shape
+    q = torch.empty((E, N, K), dtype=FP8, device=w.device)
+    s = torch.empty((E, (N + 127) // 128, (K + 127) // 128), dtype=torch.float32, device=w.device)
+    check(lib().moe_quant_block128(_ptr(w), E, N, K, _ptr(q), _ptr(s), _stream()), "moe_quant_block128")
+    return q, s
+
+
+# ---------------------------------------------------------------------------
+# A3 -- moe_align_block_size
+# ---------------------------------------------------------------------------
+
+def align_max_padded(num_slots: int, num_experts: int, block_size: int) -> int:
+    return int(lib().moe_align_max_padded(num_slots, num_experts, block_size))
+
+
+def align_workspace_bytes(num_slots: int, num_experts: int) -> int:
+    return int(lib().moe_align_workspace_bytes(num_slots, num_experts))
+
+
+class AlignBuffers:
+    """Preallocated outputs + workspace of moe_align_block_size for S slots."""
+
+    def __init__(self, num_slots: int, num_experts: int, block_size: int, device: Any):
+        self.S, self.E, self.BM = num_slots, num_experts, block_size
+        self.max_padded = align_max_padded(num_slots, num_experts, block_size)
+        self.max_blocks = (self.max_padded + block_size - 1) // block_size
+        self.sorted_ids = torch.empty(max(self.max_padded, 1), dtype=torch.int32, device=device)
+        self.expert_ids = torch.empty(max(self.max_blocks, 1), dtype=torch.int32, device=device)
+        self.ntpp = torch.empty(1, dtype=torch.int32, device=device)
+        self.workspace = torch.empty(align_workspace_bytes(num_slots, num_experts), dtype=torch.uint8,
+                                     device=device)
+
+    def run(self, topk_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        _need(topk_ids, "topk_ids", torch.int32)
+        if topk_ids.numel() != self.S:
+            raise ValueError(f"topk_ids has {topk_ids.numel()} slots, buffers were sized for {self.S}")
+        check(lib().moe_align_block_size(_ptr(topk_ids), self.S, self.E, self.BM, _ptr(self.sorted_ids),
+                                         _ptr(self.expert_ids), _ptr(self.ntpp), self.max_padded,
+                                         _ptr(self.workspace), _stream()), "moe_align_block_size")
+        return self.sorted_ids[: self.max_padded], self.expert_ids[: self.max_blocks], self.ntpp
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int,
+                         expert_map: torch.Tensor | None = None):
+    """vLLM's moe_align_block_size(topk_ids, BM, E, expert_map) as called at
+    overlap/overlap_forward.py:165-169 -> (sorted_token_ids, expert_ids,
+    num_tokens_post_padded).  Stable order within each expert, pad value S."""
+    if expert_map is not None:
+        raise NotImplementedError("expert_map (expert parallelism) is outside the single-GPU path")
+    bufs = AlignBuffers(topk_ids.numel(), num_experts, block_size, topk_ids.device)
+    return bufs.run(topk_ids.contiguous())
+
+
+# ---------------------------------------------------------------------------
+# A5 / A8 -- grouped GEMM;  A5+A6+A7 fused
+# ---------------------------------------------------------------------------
+
+def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                              A_scale: torch.Tensor, B_scale: torch.Tensor, B_zp: Any,
+                              topk_weights: torch.Tensor | None, sorted_token_ids: torch.Tensor,
+                              expert_ids: torch.Tensor, num_tokens_post_padded: torch.Tensor,
+                              mul_routed_weight: bool, top_k: int, config: dict | None = None,
+                              compute_type: Any = None, use_fp8_w8a8: bool = True,
+                              use_int8_w8a8: bool = False, use_int8_w8a16: bool = False,
+                              use_int4_w4a16: bool = False, per_channel_quant: bool = False,
+                              block_shape: list[int] | None = None, B_bias: Any = None,
+                              a_by_pos: bool = False) -> None:
+    """The reference's grouped-GEMM call (overlap/kernels.py:288-310,
+    schemes/shared_expert.py:102-123) on the FP8 w8a8 block-[128,128] form.
+    C is [M, top_k, N] or [S, 1, N]; rows are written by slot."""
+    if not use_fp8_w8a8 or use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or per_channel_quant:
+        raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
+    if B_zp is not None or B_bias is not None:
+        raise NotImplementedError("zero points / bias are not on this path")
+    if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
+        raise NotImplementedError("only block_shape [128,128]")
+    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
+                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
+        _need(t, name)
+    E, N, K = B.shape
+    S = C.numel() // N
+    BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
+    w = None
+    if mul_routed_weight:
+        if topk_weights is None:
+            raise ValueError("mul_routed_weight requires topk_weights")
+        w = topk_weights.contiguous().view(-1)
+    check(lib().moe_grouped_gemm(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids),
+                                 _ptr(expert_ids), _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
+                                 1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(), _ptr(C),
+                                 _stream()), "moe_grouped_gemm")
+
+
+def _block_m_from(sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor) -> int:
+    n, b = sorted_token_ids.numel(), expert_ids.numel()
+    for bm in SUPPORTED_BLOCK_M:
+        if (n + bm - 1) // bm == b:
+            return bm
+    raise ValueError("cannot infer BLOCK_SIZE_M; pass config={'BLOCK_SIZE_M': ...}")
+
+
+def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tensor,
+                        w13_scale: torch.Tensor, sorted_token_ids: torch.Tensor,
+                        expert_ids: torch.Tensor, num_tokens_post_padded: torch.Tensor,
+                        num_slots: int, top_k: int, block_size_m: int,
+                        hq: torch.Tensor | None = None, hs: torch.Tensor | None = None):
+    """W13 GEMM + SiLU*up + 1x128 quant of h, outputs by sorted position:
+    (hq [max_padded, I] e4m3fn, hs [max_padded, I/128] fp32)."""
+    E, N2, H = w13.shape
+    I = N2 // 2
+    max_padded = sorted_token_ids.numel()
+    if hq is None:
+        hq = torch.empty((max_padded, I), dtype=FP8, device=Aq.device)
+    if hs is None:
+        hs = torch.empty((max_padded, I // 128), dtype=torch.float32, device=Aq.device)
+    check(lib().moe_gemm_w13_silu_quant(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
+                                        _ptr(sorted_token_ids), _ptr(expert_ids),
+                                        _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
+                                        block_size_m, max_padded, _ptr(hq), _ptr(hs), _stream()),
+          "moe_gemm_w13_silu_quant")
+    return hq, hs
+
+
+# ---------------------------------------------------------------------------
+# A6 / A9
+# ---------------------------------------------------------------------------
+
+def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
+    """torch.ops._C.silu_and_mul(out, x): out[r,j] = silu(x[r,j]) * x[r,I+j]
+    (overlap/overlap_forward.py:277-279)."""
+    _need(x, "x", torch.bfloat16)
+    _need(out, "out", torch.bfloat16)
+    R = x.numel() // x.shape[-1]
+    I = x.shape[-1] // 2
+    check(lib().moe_silu_and_mul(_ptr(x), R, I, _ptr(out), _stream()), "moe_silu_and_mul")
+
+
+def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int) -> torch.Tensor:
+    """out[t] = sum_i D[t*k+i] (fp32 accumulation, bf16 result), the reference's
+    torch.sum(C_down.view(T,k,H), dim=1) (overlap/overlap_forward.py:304-313)."""
+    _need(D, "D", torch.bfloat16)
+    _need(out, "out", torch.bfloat16)
+    T, H = out.shape
+    check(lib().moe_reduce_topk(_ptr(D), T, top_k, H, _ptr(out), _stream()), "moe_reduce_topk")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# A4 -- tile configuration
+# ---------------------------------------------------------------------------
+
+def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, int]:
+    """Replacement for vLLM's try_get_optimal_moe_config (overlap_forward.py:
+    153-163): picks BLOCK_SIZE_M from the average rows per expert so that the
+    padding of small experts stays below one 16-row MFMA tile where possible."""
+    avg = num_tokens * top_k / max(num_experts, 1)
+    if avg <= 16:
+        bm = 16
+    elif avg <= 48:
+        bm = 32
+    elif avg <= 160:
+        bm = 64
+    else:
+        bm = 128
+    return {"BLOCK_SIZE_M": bm, "BLOCK_SIZE_N": 256, "BLOCK_SIZE_K": 128}
+
+
+# ---------------------------------------------------------------------------
+# A10 -- the whole layer
+# ---------------------------------------------------------------------------
+
+class FusedExpertsRunner:
+    """Prebuilt A1->A9 chain for fixed (T, H, I, E, top_k, BM).
+
+    Construction allocates every buffer; ``run`` only enqueues kernels
+    (quant -> align -> W13+SiLU+quant -> W2 with routed weights -> top-k sum)
+    on the current stream and returns the [T, H] bf16 output buffer."""
+
+    def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
+                 w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None):
+        for name, t in (("w13", w13), ("w2", w2)):
+            _need(t, name, FP8)
+        _need(w13_scale, "w13_scale", torch.float32)
+        _need(w2_scale, "w2_scale", torch.float32)
+        E, N2, H = w13.shape
+        if w2.shape != (E, H, N2 // 2):
+            raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+        self.E, self.H, self.I, self.T, self.top_k = E, H, N2 // 2, num_tokens, top_k
+        self.S = num_tokens * top_k
+        self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
+        if self.BM not in SUPPORTED_BLOCK_M:
+            raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
+        self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
+        dev = w13.device
+        self.q1 = torch.empty((self.T, H), dtype=FP8, device=dev)
+        self.s1 = torch.empty((self.T, H // 128), dtype=torch.float32, device=dev)
+        self.align = AlignBuffers(self.S, E, self.BM, dev)
+        mp = max(self.align.max_padded, 1)
+        self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
+        self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
+        self.D = torch.empty((max(self.S, 1), H), dtype=torch.bfloat16, device=dev)
+        self.y = torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
+
+    def stage_quant(self, hidden: torch.Tensor) -> None:
+        _need(hidden, "hidden_states", torch.bfloat16)
+        if tuple(hidden.shape) != (self.T, self.H):
+            raise ValueError(f"hidden_states must be [{self.T}, {self.H}]")
+        check(lib().moe_quant_group128(_ptr(hidden), self.T, self.H, _ptr(self.q1), _ptr(self.s1),
+                                       _stream()), "moe_quant_group128")
+
+    def stage_align(self, topk_ids: torch.Tensor) -> None:
+        self.align.run(topk_ids)
+
+    def stage_w13(self) -> None:
+        a = self.align
+        check(lib().moe_gemm_w13_silu_quant(_ptr(self.q1), _ptr(self.s1), _ptr(self.w13),
+                                            _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
+                                            _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
+                                            self.BM, a.max_padded, _ptr(self.hq), _ptr(self.hs),
+                                            _stream()), "moe_gemm_w13_silu_quant")
+
+    def stage_w2(self, topk_weights: torch.Tensor) -> None:
+        _need(topk_weights, "topk_weights", torch.float32)
+        a = self.align
+        check(lib().moe_grouped_gemm(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
+                                     _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
+                                     _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
+                                     a.max_padded, _ptr(self.D), _stream()), "moe_grouped_gemm")
+
+    def stage_reduce(self) -> None:
+        check(lib().moe_reduce_topk(_ptr(self.D), self.T, self.top_k, self.H, _ptr(self.y), _stream()),
+              "moe_reduce_topk")
+
+    def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
+        self.stage_quant(hidden)
+        self.stage_align(topk_ids)
+        self.stage_w13()
+        self.stage_w2(topk_weights)
+        self.stage_reduce()
+        return self.y
+
+
+def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                  topk_weights: torch.Tensor, topk_ids: torch.Tensor, global_num_experts: int = -1,
+                  w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
+                  block_size_m: int | None = None, quant_config: Any = None) -> torch.Tensor:
+    """vLLM ``fused_experts`` as the reference calls it (schemes/vllm_tp.py:
+    189-197) for FP8 w8a8 with [128,128] weight blocks.  Scales come either as
+    keywords or from ``quant_config`` (attributes ``w1_scale``/``w2_scale``).
+    Allocates per call; prebuild a FusedExpertsRunner for timed loops."""
+    if quant_config is not None:
+        w1_scale = getattr(quant_config, "w1_scale", w1_scale)
+        w2_scale = getattr(quant_config, "w2_scale", w2_scale)
+    if w1_scale is None or w2_scale is None:
+        raise ValueError("fused_experts needs w1_scale and w2_scale")
+    if global_num_experts not in (-1, w1.shape[0]):
+        raise NotImplementedError("global_num_experts != local experts needs an expert_map")
+    T, k = topk_ids.shape
+    runner = FusedExpertsRunner(w1, w1_scale, w2, w2_scale, T, k, block_size_m)
+    return runner.run(hidden_states.contiguous(), topk_weights.contiguous().view(-1),
+                      topk_ids.contiguous().view(-1)).clone()

@@ -1,0 +1,314 @@
+"""GPU parity of every kernel on the path against the CPU oracle, through the
+C ABI (td_benchmark_amd.ops -> libmoe_mi355x.so).
+
+Bars: bit-exact for the integer/byte stages (align, quant codes and scales,
+top-k reduce given identical inputs); FP8 codes of the fused intermediate
+within 1 e4m3 ULP on <= 0.1% of codes; bf16 GEMM outputs within 1 bf16 ULP
+(the kernel and the oracle both accumulate fp32 but in different orders).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from moe_cases import bf16_bits, e4m3_ulp_diff, make_case, to_gpu, u8_bits
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _ops():
+    from td_benchmark_amd import ops
+    return ops
+
+
+def _log(msg: str) -> None:
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------- MFMA layout
+
+def test_mfma_probe_layout_matches_matmul():
+    from td_benchmark_amd._lib import check, lib
+    import ctypes
+    rng = np.random.default_rng(1)
+    codes = np.arange(256, dtype=np.uint8)
+    finite = codes[(codes & 0x7F) != 0x7F]
+    A = rng.choice(finite, size=(16, 128)).astype(np.uint8)
+    B = rng.choice(finite, size=(16, 128)).astype(np.uint8)
+    lut = oracle.e4m3_lut().astype(np.float64)
+    ref = lut[A] @ lut[B].T
+    dA = torch.from_numpy(A).cuda()
+    dB = torch.from_numpy(B).cuda()
+    dC = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
+    _log("mfma probe 16x16x128")
+    check(lib().moe_debug_mfma_probe(ctypes.c_void_p(dA.data_ptr()), ctypes.c_void_p(dB.data_ptr()),
+                                     ctypes.c_void_p(dC.data_ptr()), None), "probe")
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6 * np.abs(ref).max())
+
+
+# ---------------------------------------------------------------- A1 quant
+
+@pytest.mark.parametrize("T,H,scale", [(1, 128, 1.0), (7, 256, 1.0), (64, 7168, 1.0),
+                                       (33, 2048, 1e-3), (16, 512, 300.0)])
+def test_quant_group128_bit_exact(T, H, scale):
+    ops = _ops()
+    rng = np.random.default_rng(T * 1000 + H)
+    x = oracle.f32_to_bf16(rng.standard_normal((T, H), dtype=np.float32) * np.float32(scale))
+    x[0, :128] = 0                       # all-zero group -> scale 1e-12, codes 0
+    if T > 2:
+        x[1, 5] = oracle.f32_to_bf16(np.float32(50.0 * scale))  # dominant element -> 448
+    q_ref, s_ref = oracle.quant_group128(x)
+    dx = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
+    _log(f"quant_group128 T={T} H={H}")
+    q, s = ops.per_token_group_quant_fp8(dx)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u8_bits(q), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quant_group128_conversion_sweep():
+    """Every fp32 the converter can see on the path: x/scale for a fixed
+    scale of 1 covers e4m3 values, their midpoints, +-1 ulp around each, and
+    the subnormal range; all must round exactly as the oracle does."""
+    ops = _ops()
+    lut = oracle.e4m3_lut()
+    vals = lut[np.isfinite(lut)].astype(np.float32)
+    vals = np.unique(vals)
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    pts = np.concatenate([vals, mids, np.nextafter(mids, np.float32(np.inf)),
+                          np.nextafter(mids, np.float32(-np.inf))])
+    pts = pts[np.abs(pts) <= 448.0]
+    # bf16 inputs with amax 448 -> scale exactly 1.0: round pts to bf16 first
+    xb = oracle.f32_to_bf16(pts)
+    n = ((xb.size + 126) // 127) * 127
+    xb = np.resize(xb, n).reshape(-1, 127)
+    full = np.concatenate([xb, np.full((xb.shape[0], 1), oracle.f32_to_bf16(np.float32(448.0)),
+                                       np.uint16)], axis=1)
+    q_ref, s_ref = oracle.quant_group128(full)
+    assert np.all(s_ref == 1.0)
+    dx = torch.from_numpy(np.ascontiguousarray(full).view(np.int16)).cuda().view(torch.bfloat16)
+    _log(f"quant conversion sweep rows={full.shape[0]}")
+    q, s = ops.per_token_group_quant_fp8(dx)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u8_bits(q), q_ref)
+
+
+def test_quant_block128_bit_exact():
+    ops = _ops()
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((3, 384, 256), dtype=np.float32) * np.float32(0.02)
+    w[1, :128, :128] = 0.0
+    q_ref, s_ref = oracle.quant_block128(w)
+    _log("quant_block128 (3,384,256)")
+    q, s = ops.quantize_block128(torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u8_bits(q), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+# ---------------------------------------------------------------- A3 align
+
+ALIGN_CASES = [
+    # (T, k, E, BM, routing)
+    (64, 2, 8, 64, "softmax"),
+    (64, 2, 8, 16, "softmax"),
+    (1, 1, 4, 16, "softmax"),
+    (3, 2, 256, 128, "softmax"),      # S < E
+    (128, 8, 256, 16, "zipf"),        # decode, many empty experts
+    (500, 4, 16, 32, "one_expert"),
+    (2048, 8, 256, 128, "sigmoid"),
+    (8192, 8, 256, 128, "sigmoid"),   # DSv3 size, S = 65536
+    (4096, 8, 128, 64, "softmax"),    # multiple chunks, E=128
+    (1000, 3, 1000, 32, "softmax"),   # E close to the 1024 limit
+]
+
+
+@pytest.mark.parametrize("T,k,E,BM,routing", ALIGN_CASES)
+def test_moe_align_bit_exact(T, k, E, BM, routing):
+    from moe_cases import route
+    ops = _ops()
+    rng = np.random.default_rng(T + E)
+    ids, _ = route(rng.standard_normal((T, E), dtype=np.float32), k, routing, rng)
+    sorted_ref, eids_ref, ntpp_ref = oracle.moe_align(ids, E, BM)
+    _log(f"align T={T} k={k} E={E} BM={BM} {routing}")
+    bufs = ops.AlignBuffers(T * k, E, BM, torch.device("cuda"))
+    d_ids = torch.from_numpy(ids).cuda()
+    for _ in range(2):  # twice: deterministic, and no state carried between calls
+        sorted_ids, eids, ntpp = bufs.run(d_ids)
+        torch.cuda.synchronize()
+        assert int(ntpp.item()) == ntpp_ref
+        np.testing.assert_array_equal(sorted_ids.cpu().numpy(), sorted_ref)
+        np.testing.assert_array_equal(eids.cpu().numpy(), eids_ref)
+
+
+def test_moe_align_drops_out_of_range_experts():
+    ops = _ops()
+    ids = np.array([[0, 3], [-1, 1], [7, 3], [2, 9]], np.int32)  # E = 4: -1, 7, 9 dropped
+    sorted_ref, eids_ref, ntpp_ref = oracle.moe_align(ids, 4, 16)
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(torch.from_numpy(ids).cuda(), 16, 4)
+    torch.cuda.synchronize()
+    assert int(ntpp.item()) == ntpp_ref == 64
+    np.testing.assert_array_equal(sorted_ids.cpu().numpy(), sorted_ref)
+    np.testing.assert_array_equal(eids.cpu().numpy(), eids_ref)
+
+
+# ---------------------------------------------------------------- GEMMs
+
+GEMM_CASES = [
+    # (T, H, I, E, k, BM, routing)
+    (64, 256, 512, 8, 2, 64, "softmax"),     # config 1 (tiny)
+    (64, 256, 512, 8, 2, 128, "softmax"),
+    (64, 256, 512, 8, 2, 16, "softmax"),
+    (37, 384, 384, 16, 3, 32, "zipf"),       # ragged T, odd group counts
+    (256, 1024, 768, 32, 4, 64, "softmax"),
+    (128, 2048, 256, 64, 8, 16, "zipf"),
+]
+
+
+def _bf16_close(got: np.ndarray, ref: np.ndarray, ulps: int = 1):
+    g = oracle.bf16_to_f32(got).astype(np.float64)
+    r = oracle.bf16_to_f32(ref).astype(np.float64)
+    tol = ulps * np.maximum(np.abs(r), 1e-30) * 2.0 ** -7 + 1e-30
+    bad = np.abs(g - r) > tol
+    assert bad.sum() == 0, f"{bad.sum()} of {bad.size} bf16 values differ by more than {ulps} ulp"
+
+
+@pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
+def test_grouped_gemm_w13_plain(T, H, I, E, k, BM, routing):
+    ops = _ops()
+    c = make_case(T, H, I, E, k, BM, seed=T + H, routing=routing)
+    q1, s1 = oracle.quant_group128(c.x)
+    sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, E, BM)
+    ref = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k)
+    g = to_gpu(c)
+    _log(f"gemm w13 plain T={T} H={H} I={I} E={E} k={k} BM={BM}")
+    dq = torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn)
+    ds = torch.from_numpy(s1).cuda()
+    d_sorted = torch.from_numpy(sorted_ids).cuda()
+    d_eids = torch.from_numpy(eids).cuda()
+    d_ntpp = torch.tensor([ntpp], dtype=torch.int32, device="cuda")
+    C = torch.zeros((T, k, 2 * I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(dq, g["w13"], C, ds, g["w13_s"], None, None, d_sorted, d_eids, d_ntpp,
+                                  False, k, {"BLOCK_SIZE_M": BM}, block_shape=[128, 128])
+    torch.cuda.synchronize()
+    _bf16_close(bf16_bits(C).reshape(c.S, 2 * I), ref)
+
+
+@pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
+def test_w13_fused_silu_quant(T, H, I, E, k, BM, routing):
+    """Fused W13 epilogue == unfused chain on the GPU (bit-exact), and within
+    1 e4m3 ULP on <= 0.1% of codes of the CPU oracle chain."""
+    ops = _ops()
+    c = make_case(T, H, I, E, k, BM, seed=T * 7 + I, routing=routing)
+    st = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, BM)
+    g = to_gpu(c)
+    _log(f"w13 fused T={T} H={H} I={I} E={E} k={k} BM={BM}")
+    q1, s1 = ops.per_token_group_quant_fp8(g["x"])
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(g["topk_ids"], BM, E)
+    hq, hs = ops.gemm_w13_silu_quant(q1, s1, g["w13"], g["w13_s"], sorted_ids, eids, ntpp, c.S, k, BM)
+    # unfused GPU chain
+    C = torch.empty((c.S, 2 * I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(q1, g["w13"], C, s1, g["w13_s"], None, None, sorted_ids, eids, ntpp,
+                                  False, k, {"BLOCK_SIZE_M": BM})
+    h = torch.empty((c.S, I), dtype=torch.bfloat16, device="cuda")
+    ops.silu_and_mul(h, C)
+    q2, s2 = ops.per_token_group_quant_fp8(h)
+    torch.cuda.synchronize()
+    ntpp_v = int(ntpp.item())
+    assert ntpp_v == st["ntpp"]
+    srt = sorted_ids.cpu().numpy()[:ntpp_v]
+    valid = srt < c.S
+    pos = np.nonzero(valid)[0]
+    slots = srt[valid]
+    hq_np = u8_bits(hq)[pos]
+    hs_np = hs.cpu().numpy()[pos]
+    # 1) fused == unfused GPU chain, bit-exact
+    np.testing.assert_array_equal(hq_np, u8_bits(q2)[slots])
+    np.testing.assert_array_equal(hs_np, s2.cpu().numpy()[slots])
+    # 2) vs oracle: <= 1 ulp on <= 0.1% of codes
+    d = e4m3_ulp_diff(hq_np, st["q2"][slots])
+    assert d.max() <= 1, f"max code diff {d.max()} ulp"
+    assert (d > 0).mean() <= 1e-3, f"{(d > 0).mean():.2e} of codes differ"
+    srel = np.abs(hs_np - st["s2"][slots]) / st["s2"][slots]
+    assert (srel > 0).mean() <= 1e-2 and srel.max() <= 2.0 ** -7
+
+
+@pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
+def test_grouped_gemm_w2_routed(T, H, I, E, k, BM, routing):
+    """W2 GEMM reading A by sorted position, routed weights in the epilogue."""
+    ops = _ops()
+    c = make_case(T, H, I, E, k, BM, seed=T * 3 + H, routing=routing)
+    rng = np.random.default_rng(5)
+    sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, E, BM)
+    mp = sorted_ids.size
+    hq = rng.integers(0, 256, size=(mp, I), dtype=np.uint8)
+    hq[(hq & 0x7F) == 0x7F] = 0
+    hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
+    ref = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
+                              a_row_by_pos=True, topk_w=c.topk_w.ravel())
+    g = to_gpu(c)
+    _log(f"gemm w2 T={T} H={H} I={I} E={E} k={k} BM={BM}")
+    D = torch.zeros((c.S, 1, H), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(torch.from_numpy(hq).cuda().view(torch.float8_e4m3fn), g["w2"], D,
+                                  torch.from_numpy(hs).cuda(), g["w2_s"], None, g["topk_w"],
+                                  torch.from_numpy(sorted_ids).cuda(), torch.from_numpy(eids).cuda(),
+                                  torch.tensor([ntpp], dtype=torch.int32, device="cuda"), True, 1,
+                                  {"BLOCK_SIZE_M": BM}, a_by_pos=True)
+    torch.cuda.synchronize()
+    _bf16_close(bf16_bits(D).reshape(c.S, H), ref)
+
+
+def test_grouped_gemm_expert_minus_one_writes_zeros():
+    ops = _ops()
+    c = make_case(32, 256, 256, 4, 2, 16, seed=11)
+    q1, s1 = oracle.quant_group128(c.x)
+    sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, 4, 16)
+    eids = eids.copy()
+    eids[0] = -1
+    g = to_gpu(c)
+    C = torch.full((c.S, 512), 7.0, dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn), g["w13"], C,
+                                  torch.from_numpy(s1).cuda(), g["w13_s"], None, None,
+                                  torch.from_numpy(sorted_ids).cuda(), torch.from_numpy(eids).cuda(),
+                                  torch.tensor([ntpp], dtype=torch.int32, device="cuda"), False, 2,
+                                  {"BLOCK_SIZE_M": 16})
+    torch.cuda.synchronize()
+    out = C.float().cpu().numpy()
+    first_block_slots = sorted_ids[:16][sorted_ids[:16] < c.S]
+    assert first_block_slots.size > 0
+    assert np.all(out[first_block_slots] == 0.0)
+
+
+# ---------------------------------------------------------------- A6, A9
+
+def test_silu_and_mul_matches_oracle():
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    c = oracle.f32_to_bf16(rng.standard_normal((300, 2 * 384), dtype=np.float32) * 3)
+    ref = oracle.silu_and_mul(c)
+    d = torch.from_numpy(c.view(np.int16)).cuda().view(torch.bfloat16)
+    h = torch.empty((300, 384), dtype=torch.bfloat16, device="cuda")
+    ops.silu_and_mul(h, d)
+    torch.cuda.synchronize()
+    got = bf16_bits(h)
+    diff = got != ref
+    assert diff.mean() <= 1e-3
+    _bf16_close(got, ref, ulps=1)
+
+
+@pytest.mark.parametrize("T,k,H", [(64, 2, 256), (100, 8, 7168), (3, 1, 128), (17, 32, 1024)])
+def test_reduce_topk_bit_exact(T, k, H):
+    ops = _ops()
+    rng = np.random.default_rng(T * k)
+    D = oracle.f32_to_bf16(rng.standard_normal((T * k, H), dtype=np.float32))
+    ref = oracle.moe_reduce(D, T, k)
+    dD = torch.from_numpy(D.view(np.int16)).cuda().view(torch.bfloat16)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ops.moe_sum(dD, y, k)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bf16_bits(y), ref)
