@@ -77,7 +77,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_dequant_block128.argtypes = [P, P, i64, i64, i64, P]
     L.oracle_moe_align.argtypes = [P, i64, i32, i32, P, P, P, i64]
     L.oracle_moe_align.restype = ctypes.c_int
-    L.oracle_grouped_gemm.argtypes = [P, P, P, P, P, P, i32, i32, i64, i32, i64, i64, i32, P, P]
+    L.oracle_grouped_gemm.argtypes = [P, P, P, P, P, P, i32, i32, i64, i32, i64, i64, i32, P, P, P]
     L.oracle_silu_and_mul.argtypes = [P, i64, i64, P]
     L.oracle_moe_reduce.argtypes = [P, i64, i32, i64, P]
 
@@ -193,9 +193,11 @@ def moe_align(topk_ids: np.ndarray, E: int, BM: int, max_padded: int | None = No
 
 
 def grouped_gemm(A, a_s, B, b_s, sorted_ids, expert_ids, ntpp, BM, S, top_k,
-                 a_row_by_pos=False, topk_w=None) -> np.ndarray:
+                 a_row_by_pos=False, topk_w=None, with_magnitude=False):
     """A5/A8: block-scaled FP8 grouped GEMM -> bf16 bits [S, N] (rows by slot;
-    rows of slots never placed stay 0).  Reference: overlap/kernels.py:95-214."""
+    rows of slots never placed stay 0).  Reference: overlap/kernels.py:95-214.
+    With ``with_magnitude`` also returns fp32 [S, N] L1 magnitudes
+    |w| * sum_kb sum_k |a*b| * a_s * b_s (see moe_oracle.c)."""
     A = _c(A, np.uint8)
     a_s = _c(a_s, np.float32)
     B = _c(B, np.uint8)
@@ -204,11 +206,26 @@ def grouped_gemm(A, a_s, B, b_s, sorted_ids, expert_ids, ntpp, BM, S, top_k,
     expert_ids = _c(expert_ids, np.int32)
     E, N, K = B.shape
     out = np.zeros((S, N), np.uint16)
+    mag = np.zeros((S, N), np.float32) if with_magnitude else None
     w = None if topk_w is None else _c(topk_w, np.float32).ravel()
     lib().oracle_grouped_gemm(_ptr(A), _ptr(a_s), _ptr(B), _ptr(b_s), _ptr(sorted_ids),
                               _ptr(expert_ids), int(ntpp), BM, S, top_k, N, K,
-                              1 if a_row_by_pos else 0, _ptr(w), _ptr(out))
-    return out
+                              1 if a_row_by_pos else 0, _ptr(w), _ptr(out), _ptr(mag))
+    return (out, mag) if with_magnitude else out
+
+
+# Reduced-precision accumulation inside one FP8 MFMA 128-element dot: the
+# observed error on gfx950 is <= 2^-14.2 of the dot's L1 size; GEMM parity
+# tests allow 2^-12 of it (plus one bf16 ulp of the result).
+MFMA_L1_REL = 2.0 ** -12
+
+
+def gemm_close(got_bf16: np.ndarray, ref_bf16: np.ndarray, mag: np.ndarray) -> np.ndarray:
+    """Boolean mask of outputs violating |got-ref| <= 2^-7|ref| + MFMA_L1_REL*mag."""
+    g = bf16_to_f32(got_bf16).astype(np.float64)
+    r = bf16_to_f32(ref_bf16).astype(np.float64)
+    tol = 2.0 ** -7 * np.abs(r) + MFMA_L1_REL * mag.astype(np.float64) + 1e-30
+    return np.abs(g - r) > tol
 
 
 def silu_and_mul(c_bf16: np.ndarray) -> np.ndarray:

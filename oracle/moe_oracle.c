@@ -77,8 +77,6 @@ uint16_t oracle_f32_to_bf16(float f) {
 
 float oracle_bf16_to_f32(uint16_t b) { return u2f(((uint32_t)b) << 16); }
 
-static inline float bf16r(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16(f)); }
-
 /* ---------------------------------------------------------------------------
  * A1 / A7: dynamic 1x128 per-token-group activation quant.
  * Follows verify.py:108-117 (_group_quant_dequant) for the arithmetic:
@@ -232,13 +230,16 @@ int oracle_moe_align(const int32_t* ids, int64_t S, int32_t E, int32_t BM,
  *   out[s, n] = bf16(acc_n)                       (kernels.py:198-210)
  * A: fp8 codes [rows, K]; a_s [rows, ceil(K/128)]; B: [E, N, K]; b_s
  * [E, ceil(N/128), ceil(K/128)].  out: bf16 bits [S, N] (rows by slot).
+ * mag (nullable): fp32 [S, N], |w| * sum_kb (sum_k |A*B|) * a_s * b_s -- the
+ * L1 size of the products behind each output, which bounds the effect of an
+ * inexact (reduced-precision) accumulation inside one 128-element dot.
  * ------------------------------------------------------------------------- */
 void oracle_grouped_gemm(const uint8_t* A, const float* a_s, const uint8_t* B,
                          const float* b_s, const int32_t* sorted,
                          const int32_t* expert_ids, int32_t ntpp, int32_t BM,
                          int64_t S, int32_t top_k, int64_t N, int64_t K,
                          int32_t a_row_by_pos, const float* topk_w,
-                         uint16_t* out) {
+                         uint16_t* out, float* mag) {
     int64_t KB = (K + 127) / 128, NB = (N + 127) / 128;
     float lut[256];
     for (int i = 0; i < 256; ++i) lut[i] = oracle_e4m3_to_f32((uint8_t)i);
@@ -251,17 +252,28 @@ void oracle_grouped_gemm(const uint8_t* A, const float* a_s, const uint8_t* B,
         for (int64_t n = 0; n < N; ++n) {
             const uint8_t* w = B + ((int64_t)e * N + n) * K;
             float acc = 0.0f;
+            double l1 = 0.0;
             for (int64_t kb = 0; kb < KB; ++kb) {
-                double dot = 0.0;
+                double dot = 0.0, dabs = 0.0;
                 int64_t k1 = (kb + 1) * 128 < K ? (kb + 1) * 128 : K;
-                for (int64_t k = kb * 128; k < k1; ++k)
-                    dot += (double)lut[a[k]] * (double)lut[w[k]];
-                float t = (float)dot * a_s[row * KB + kb];
-                t = t * b_s[((int64_t)e * NB + n / 128) * KB + kb];
+                for (int64_t k = kb * 128; k < k1; ++k) {
+                    double p = (double)lut[a[k]] * (double)lut[w[k]];
+                    dot += p;
+                    dabs += fabs(p);
+                }
+                float sa = a_s[row * KB + kb];
+                float sb = b_s[((int64_t)e * NB + n / 128) * KB + kb];
+                float t = (float)dot * sa;
+                t = t * sb;
                 acc = acc + t;
+                l1 += dabs * (double)sa * (double)sb;
             }
-            if (topk_w) acc = acc * topk_w[s];
+            if (topk_w) {
+                acc = acc * topk_w[s];
+                l1 *= fabs((double)topk_w[s]);
+            }
             out[s * N + n] = oracle_f32_to_bf16(acc);
+            if (mag) mag[s * N + n] = (float)l1;
         }
     }
 }

@@ -54,20 +54,26 @@ MOE_DEVICE float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f
 // Correctly rounded x / s given inv = RN(1/s): q0 = RN(x*inv); the residual
 // x - q0*s is exact under fma; one correction step gives RN(x/s) (Markstein's
 // final-step theorem for round-to-nearest, valid away from overflow and
-// subnormal quotients; see the quant tests for the exhaustive CPU check).
+// subnormal quotients).  The sign is copied from x so that -0 / s stays -0
+// (the correction step alone would return +0 for x = -0).  s > 0 always.
 MOE_DEVICE float div_by(float x, float s, float inv) {
   float q0 = x * inv;
   float r = __builtin_fmaf(-q0, s, x);
-  return __builtin_fmaf(r, inv, q0);
+  return __builtin_copysignf(__builtin_fmaf(r, inv, q0), x);
 }
 
 MOE_DEVICE float clamp_fp8(float v) { return __builtin_amdgcn_fmed3f(v, -kFp8Max, kFp8Max); }
 
 // Four fp32 (already clamped to +-448) -> four packed e4m3fn bytes, RNE.
+// The hardware conversion returns +0 for a negative input that rounds to
+// zero, where OCP e4m3fn (and torch's cast) keep the sign (-0 = 0x80): each
+// input's sign bit is ORed into its byte, a no-op for non-zero results.
 MOE_DEVICE uint32_t pack4_e4m3(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-  return (uint32_t)w;
+  const uint32_t sg = ((__float_as_uint(a) >> 24) & 0x80u) | ((__float_as_uint(b) >> 16) & 0x8000u) |
+                      ((__float_as_uint(c) >> 8) & 0x800000u) | (__float_as_uint(d) & 0x80000000u);
+  return (uint32_t)w | sg;
 }
 
 // Group scale of verify.py:115: max(amax / 448, 1e-12), IEEE division.

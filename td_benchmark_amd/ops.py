@@ -74,13 +74,17 @@ def moe_kernel_quantize_input(A: torch.Tensor, A_scale: torch.Tensor | None, qua
 # A2 -- 128x128 weight quant (build time)
 # ---------------------------------------------------------------------------
 
-def quantize_block128(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def quantize_block128(w: torch.Tensor, out_q: torch.Tensor | None = None,
+                      out_s: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """fp32 [E,N,K] -> (e4m3fn [E,N,K], scales [E,ceil(N/128),ceil(K/128)]),
     moe_bench/data/checkpoint.py:28-40 on the GPU."""
     _need(w, "w", torch.float32)
     E, N, K = w.shape
-    q = torch.empty((E, N, K), dtype=FP8, device=w.device)
-    s = torch.empty((E, (N + 127) // 128, (K + 127) // 128), dtype=torch.float32, device=w.device)
+    q = torch.empty((E, N, K), dtype=FP8, device=w.device) if out_q is None else out_q
+    s = (torch.empty((E, (N + 127) // 128, (K + 127) // 128), dtype=torch.float32, device=w.device)
+         if out_s is None else out_s)
+    _need(q, "out_q", FP8)
+    _need(s, "out_s", torch.float32)
     check(lib().moe_quant_block128(_ptr(w), E, N, K, _ptr(q), _ptr(s), _stream()), "moe_quant_block128")
     return q, s
 

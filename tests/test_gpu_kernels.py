@@ -48,7 +48,12 @@ def test_mfma_probe_layout_matches_matmul():
                                      ctypes.c_void_p(dC.data_ptr()), None), "probe")
     torch.cuda.synchronize()
     got = dC.cpu().numpy().astype(np.float64)
-    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6 * np.abs(ref).max())
+    # Pairing/layout errors would move results by O(L1); the hardware's own
+    # reduced-precision accumulation stays within oracle.MFMA_L1_REL of L1.
+    l1 = np.abs(lut[A]) @ np.abs(lut[B]).T
+    err = np.abs(got - ref)
+    print(f"probe max err/L1 = {(err / l1).max():.3e}", flush=True)
+    assert np.all(err <= oracle.MFMA_L1_REL * l1)
 
 
 # ---------------------------------------------------------------- A1 quant
@@ -61,7 +66,7 @@ def test_quant_group128_bit_exact(T, H, scale):
     x = oracle.f32_to_bf16(rng.standard_normal((T, H), dtype=np.float32) * np.float32(scale))
     x[0, :128] = 0                       # all-zero group -> scale 1e-12, codes 0
     if T > 2:
-        x[1, 5] = oracle.f32_to_bf16(np.float32(50.0 * scale))  # dominant element -> 448
+        x[1, 5] = oracle.f32_to_bf16(np.array([50.0 * scale], np.float32))[0]  # dominant -> 448
     q_ref, s_ref = oracle.quant_group128(x)
     dx = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
     _log(f"quant_group128 T={T} H={H}")
@@ -95,6 +100,29 @@ def test_quant_group128_conversion_sweep():
     _log(f"quant conversion sweep rows={full.shape[0]}")
     q, s = ops.per_token_group_quant_fp8(dx)
     torch.cuda.synchronize()
+    np.testing.assert_array_equal(u8_bits(q), q_ref)
+
+
+@pytest.mark.parametrize("anchor", [448.0, 1.0, 300.0, 0.0625, 1000.0])
+def test_quant_group128_every_bf16_input(anchor):
+    """Every finite bf16 bit pattern with |x| <= anchor, in groups of 127 plus
+    one anchor element (so the group scale is anchor/448, a power of two only
+    for 448): exhaustive over the inputs the converter and the division see."""
+    ops = _ops()
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = oracle.bf16_to_f32(bits)
+    keep = np.isfinite(vals) & (np.abs(vals) <= anchor)
+    xb = bits[keep]
+    n = ((xb.size + 126) // 127) * 127
+    xb = np.resize(xb, n).reshape(-1, 127)
+    a = oracle.f32_to_bf16(np.array([anchor], np.float32))[0]
+    full = np.ascontiguousarray(np.concatenate([xb, np.full((xb.shape[0], 1), a, np.uint16)], axis=1))
+    q_ref, s_ref = oracle.quant_group128(full)
+    dx = torch.from_numpy(full.view(np.int16)).cuda().view(torch.bfloat16)
+    _log(f"quant every-bf16 anchor={anchor} rows={full.shape[0]}")
+    q, s = ops.per_token_group_quant_fp8(dx)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
     np.testing.assert_array_equal(u8_bits(q), q_ref)
 
 
@@ -170,6 +198,11 @@ GEMM_CASES = [
 ]
 
 
+def _gemm_close(got: np.ndarray, ref: np.ndarray, mag: np.ndarray):
+    bad = oracle.gemm_close(got, ref, mag)
+    assert bad.sum() == 0, f"{bad.sum()} of {bad.size} outputs outside 1 bf16 ulp + MFMA L1 bound"
+
+
 def _bf16_close(got: np.ndarray, ref: np.ndarray, ulps: int = 1):
     g = oracle.bf16_to_f32(got).astype(np.float64)
     r = oracle.bf16_to_f32(ref).astype(np.float64)
@@ -184,7 +217,8 @@ def test_grouped_gemm_w13_plain(T, H, I, E, k, BM, routing):
     c = make_case(T, H, I, E, k, BM, seed=T + H, routing=routing)
     q1, s1 = oracle.quant_group128(c.x)
     sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, E, BM)
-    ref = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k)
+    ref, mag = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
+                                   with_magnitude=True)
     g = to_gpu(c)
     _log(f"gemm w13 plain T={T} H={H} I={I} E={E} k={k} BM={BM}")
     dq = torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn)
@@ -196,13 +230,15 @@ def test_grouped_gemm_w13_plain(T, H, I, E, k, BM, routing):
     ops.dispatch_fused_moe_kernel(dq, g["w13"], C, ds, g["w13_s"], None, None, d_sorted, d_eids, d_ntpp,
                                   False, k, {"BLOCK_SIZE_M": BM}, block_shape=[128, 128])
     torch.cuda.synchronize()
-    _bf16_close(bf16_bits(C).reshape(c.S, 2 * I), ref)
+    _gemm_close(bf16_bits(C).reshape(c.S, 2 * I), ref, mag)
 
 
 @pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
 def test_w13_fused_silu_quant(T, H, I, E, k, BM, routing):
-    """Fused W13 epilogue == unfused chain on the GPU (bit-exact), and within
-    1 e4m3 ULP on <= 0.1% of codes of the CPU oracle chain."""
+    """The fused epilogue equals the unfused GPU chain bit for bit; the A7
+    quant is bit-exact given h and A6 is within one bf16 ulp given C13; the
+    codes against the all-CPU chain differ only where the MFMA's internal
+    accumulation moved C13 (bounded separately by the plain GEMM test)."""
     ops = _ops()
     c = make_case(T, H, I, E, k, BM, seed=T * 7 + I, routing=routing)
     st = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, BM)
@@ -230,12 +266,20 @@ def test_w13_fused_silu_quant(T, H, I, E, k, BM, routing):
     # 1) fused == unfused GPU chain, bit-exact
     np.testing.assert_array_equal(hq_np, u8_bits(q2)[slots])
     np.testing.assert_array_equal(hs_np, s2.cpu().numpy()[slots])
-    # 2) vs oracle: <= 1 ulp on <= 0.1% of codes
+    # 2) A7 given h: the CPU quant of the GPU's h reproduces the GPU codes/scales
+    h_np = bf16_bits(h)
+    q_ref, s_ref = oracle.quant_group128(h_np)
+    np.testing.assert_array_equal(u8_bits(q2), q_ref)
+    np.testing.assert_array_equal(s2.cpu().numpy(), s_ref)
+    # 3) A6 given C13: within one bf16 ulp, bit-exact on >= 99.9%
+    h_ref = oracle.silu_and_mul(bf16_bits(C))
+    _bf16_close(h_np, h_ref, ulps=1)
+    assert (h_np != h_ref).mean() <= 1e-3
+    # 4) against the all-CPU chain (exact dots): report, and bound the tail
     d = e4m3_ulp_diff(hq_np, st["q2"][slots])
-    assert d.max() <= 1, f"max code diff {d.max()} ulp"
-    assert (d > 0).mean() <= 1e-3, f"{(d > 0).mean():.2e} of codes differ"
-    srel = np.abs(hs_np - st["s2"][slots]) / st["s2"][slots]
-    assert (srel > 0).mean() <= 1e-2 and srel.max() <= 2.0 ** -7
+    frac = (d > 0).mean()
+    _log(f"codes vs CPU chain: differ {frac:.2e}, >1ulp {(d > 1).mean():.2e}, max {d.max()}")
+    assert frac <= 1e-2
 
 
 @pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
@@ -249,8 +293,8 @@ def test_grouped_gemm_w2_routed(T, H, I, E, k, BM, routing):
     hq = rng.integers(0, 256, size=(mp, I), dtype=np.uint8)
     hq[(hq & 0x7F) == 0x7F] = 0
     hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
-    ref = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
-                              a_row_by_pos=True, topk_w=c.topk_w.ravel())
+    ref, mag = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
+                                   a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_magnitude=True)
     g = to_gpu(c)
     _log(f"gemm w2 T={T} H={H} I={I} E={E} k={k} BM={BM}")
     D = torch.zeros((c.S, 1, H), dtype=torch.bfloat16, device="cuda")
@@ -260,7 +304,7 @@ def test_grouped_gemm_w2_routed(T, H, I, E, k, BM, routing):
                                   torch.tensor([ntpp], dtype=torch.int32, device="cuda"), True, 1,
                                   {"BLOCK_SIZE_M": BM}, a_by_pos=True)
     torch.cuda.synchronize()
-    _bf16_close(bf16_bits(D).reshape(c.S, H), ref)
+    _gemm_close(bf16_bits(D).reshape(c.S, H), ref, mag)
 
 
 def test_grouped_gemm_expert_minus_one_writes_zeros():
