@@ -51,6 +51,26 @@ MOE_DEVICE uint32_t f32_to_bf16_bits(float f) {
 
 MOE_DEVICE float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
 
+// Two fp32 -> packed bf16 pair (round to nearest even, v_cvt_pk_bf16_f32);
+// a in the low half.
+MOE_DEVICE uint32_t pack_bf16x2(float a, float b) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const v2bf r = __builtin_convertvector((v2f){a, b}, v2bf);
+  return __builtin_bit_cast(uint32_t, r);
+}
+MOE_DEVICE float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
+MOE_DEVICE float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// silu(g) * u = g / (1 + exp(-g)) * u in fp32 (reciprocal form), rounded to
+// bf16.  g and u are the bf16-rounded gate / up values of the chain
+// C (bf16) -> silu_and_mul (fp32 math, bf16 out).  Shared by the standalone
+// silu_and_mul kernel and the fused W13 epilogue so the two agree bit for bit.
+MOE_DEVICE float silu_mul_bf16(float g, float u) {
+  const float s = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  return lo_bf16(pack_bf16x2(s * u, 0.0f));
+}
+
 // Correctly rounded x / s given inv = RN(1/s): q0 = RN(x*inv); the residual
 // x - q0*s is exact under fma; one correction step gives RN(x/s) (Markstein's
 // final-step theorem for round-to-nearest, valid away from overflow and

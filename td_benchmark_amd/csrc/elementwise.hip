@@ -62,11 +62,9 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __res
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t gw = (uint32_t)gv[j], uw = (uint32_t)uv[j];
-    const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xFFFF0000u);
-    const float u0 = __uint_as_float(uw << 16), u1 = __uint_as_float(uw & 0xFFFF0000u);
-    const float h0 = g0 / (1.0f + __expf(-g0)) * u0;
-    const float h1 = g1 / (1.0f + __expf(-g1)) * u1;
-    out[j] = (int)(f32_to_bf16_bits(h0) | (f32_to_bf16_bits(h1) << 16));
+    const float h0 = silu_mul_bf16(lo_bf16(gw), lo_bf16(uw));
+    const float h1 = silu_mul_bf16(hi_bf16(gw), hi_bf16(uw));
+    out[j] = (int)pack_bf16x2(h0, h1);
   }
   *reinterpret_cast<v4i*>(h + r * I + cc * 8) = out;
 }

@@ -11,34 +11,58 @@
 //     acc *= topk_w[s] if routed weights are applied           (:192-194)
 //     C[s, n] = bf16(acc)                                      (:198-210)
 // The fused W13 variant keeps gate columns [j*128, j*128+128) and up columns
-// [I + j*128, ...) of the same workgroup, and finishes in the epilogue with
-// SiLU*up (overlap_forward.py:277-279, rounding C to bf16 and h to bf16 as the
-// unfused chain does) and the 1x128 quant of h (overlap_forward.py:282-284),
-// writing FP8 codes + scales by sorted position so that W2 reads its A rows
-// contiguously.
+// [I + j*128, ...) in the same workgroup and finishes in the epilogue with
+// SiLU*up (overlap_forward.py:277-279; C rounded to bf16 and h rounded to bf16
+// as the unfused chain does) and the 1x128 quant of h (overlap_forward.py:
+// 282-284), writing FP8 codes + scales by sorted position so that the W2 GEMM
+// reads its A rows contiguously.
 //
-// Tiling (one workgroup = 4 waves = 256 threads, one expert block of BM rows,
-// 256 B-rows = two 128-row scale groups, K step 128 = one scale block):
-//   * every K step is exactly one 16x16x128 MFMA per 16x16 output subtile,
-//     started from a zero accumulator, so the per-block scales are applied as
-//     acc = fma(partial, a_s[row] * b_s[group], acc) -- no second accumulator;
-//   * A (gathered rows) and B tiles are double-buffered in LDS (BM*128 +
-//     256*128 bytes per stage), 16-byte chunks XOR-swizzled by row so that the
-//     MFMA fragment reads (two ds_read_b128 per lane) are bank-conflict free;
-//   * a lane's fragment is 32 contiguous K bytes of one row; A and B use the
-//     same K placement, so the contraction is independent of how the hardware
-//     orders K inside the instruction;
-//   * the launch is XCD-aware: workgroup ids are dealt round-robin to the 8
-//     XCDs, so consecutive ids on one XCD are mapped to the n-tiles of a small
-//     group of consecutive M blocks (same expert), which then share their A rows
-//     and weight tiles in that XCD's L2.
+// Tiling: one workgroup = 4 waves = 256 threads computes BM rows (one expert
+// block) x 256 B-rows (two 128-row scale groups); the K step is 128 = one
+// scale block, and every K step is exactly one 16x16x128 MFMA per 16x16
+// output subtile started from zero, so the per-block scales are applied as
+// acc = fma(partial, a_s[row]*b_s[group], acc) with no second accumulator.
+// The fp32 promotion at every 128-K block also bounds the matrix core's
+// reduced-precision accumulation inside one instruction.  16-row subtiles
+// that hold only padding rows (moe_align pads every expert to BM) issue no
+// MFMA at all.
+//
+// Pipeline: a 3-stage LDS ring (A BM*128 B + B 32 KiB per stage, plus the A
+// scales) filled by direct-to-LDS loads (global_load_lds_dwordx4: each lane
+// moves 16 B from its own global address -- a gathered A row -- straight into
+// LDS, no VGPR staging; addresses are a uniform base plus a fixed 32-bit lane
+// offset).  Step k waits until only step k+1's loads are in flight, passes one
+// barrier, issues step k+2's loads into the buffer freed at step k-1, then
+// computes: two K steps of memory latency hide behind MFMA work.
+//
+// LDS rows are 128 B; the 16 B chunk index of a row is XORed with
+// swz(row) = (row mod 8) ^ bit3(row), which depends only on the row's
+// position inside its 16-row MFMA subtile.  A fragment read (lane = row fr,
+// K segment kseg: 32 contiguous K bytes = two ds_read_b128) is therefore one of
+// two per-lane base addresses plus a compile-time offset for every subtile,
+// and the 8 / 16 lanes serviced together hit distinct banks.  The swizzle is
+// applied on the global side (lane L of a DMA instruction fetches the logical
+// chunk that belongs at its LDS slot).  A and B use the same K placement, so
+// the contraction does not depend on how the hardware orders K inside the
+// instruction.
+//
+// Launch: workgroup ids are dealt round-robin to the 8 XCDs; the id -> tile map
+// gives each XCD a contiguous range of an expert-major tile order, so all M
+// blocks of one expert that read the same weight tile run together on one
+// XCD (weights leave HBM once) and an M block's A rows are shared by its
+// n-tiles in that XCD's L2.
+#include <type_traits>
+
 #include "common.hpp"
+
+#define MOE_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
 namespace moe {
 
 constexpr int kGemmThreads = 256;
 constexpr int kXcds = 8;
-constexpr int kGroupM = 2;  // consecutive M blocks sharing an XCD's L2
+constexpr int kStages = 3;
+constexpr int kMaxKB = 128;  // K <= 16384
 
 template <int BM>
 struct Tile {
@@ -48,16 +72,24 @@ struct Tile {
   static constexpr int CS = 8 / WN;               // 16-col subtiles per wave per group
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = 256 * 128;
-  static constexpr int A_CHUNKS = BM * 8;
-  static constexpr int A_PER_THREAD = (A_CHUNKS + kGemmThreads - 1) / kGemmThreads;
-  static constexpr int B_PER_THREAD = 256 * 8 / kGemmThreads;
-  // LDS carve-up: [A0 A1][B0 B1][sa0 sa1][sb0 sb1 (2 floats each)][row amax WN*BM]
-  static constexpr int OFF_B = 2 * A_BYTES;
-  static constexpr int OFF_SA = OFF_B + 2 * B_BYTES;
-  static constexpr int OFF_SB = OFF_SA + 2 * BM * 4;
-  static constexpr int OFF_RED = OFF_SB + 16;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int NA = BM / 8;               // 1 KiB A DMA instructions per stage
+  static constexpr int NB = 32;                   // 1 KiB B DMA instructions per stage
+  static constexpr int NS = (BM + 63) / 64;       // 256 B A-scale DMA instructions per stage
+  static constexpr int NA_W = (NA + 3) / 4;       // A instructions of the busiest wave
+  static constexpr int na(int w) { return w < NA ? (NA - w + 3) / 4 : 0; }
+  static constexpr int ns(int w) { return (3 - w) < NS ? 1 : 0; }  // waves 3, 2 issue scales
+  static constexpr int cnt(int w) { return na(w) + NB / 4 + ns(w); }
+  static constexpr int min2(int a, int b) { return a < b ? a : b; }
+  // loads of one stage per wave that may stay in flight while the older stage is consumed
+  static constexpr int VM = min2(min2(cnt(0), cnt(1)), min2(cnt(2), cnt(3)));
+  static constexpr int OFF_SA = kStages * STAGE;
+  static constexpr int OFF_SB = OFF_SA + kStages * NS * 256;
+  static constexpr int OFF_RED = OFF_SB + 2 * kMaxKB * 4;
   static constexpr int LDS_BYTES = OFF_RED + WN * BM * 4;
-  static_assert(BM * 512 <= OFF_SA, "bf16 output staging must fit in the operand buffers");
+  static_assert(BM * 512 <= OFF_SA, "bf16 output staging must fit in the operand ring");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(VM < 16, "vmcnt immediate");
 };
 
 struct GemmArgs {
@@ -83,18 +115,36 @@ struct GemmArgs {
   int E;
 };
 
-MOE_DEVICE int swz(int row) { return (row ^ (row >> 3)) & 7; }
-
-MOE_DEVICE v8i lds_frag(const uint8_t* tile, int row, int kseg) {
-  const int sw = swz(row);
-  const v4i x = *reinterpret_cast<const v4i*>(tile + row * 128 + (((2 * kseg) ^ sw) << 4));
-  const v4i y = *reinterpret_cast<const v4i*>(tile + row * 128 + (((2 * kseg + 1) ^ sw) << 4));
-  return (v8i){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-}
+// Chunk swizzle of an LDS row (see the header comment).
+MOE_HOST_DEVICE int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// LDS slot of logical 16 B chunk c in row `row`, and its inverse (an involution).
+MOE_HOST_DEVICE int slot_of(int c, int row) { return (c ^ swz(row)) & 7; }
 
 MOE_DEVICE v4f mfma_fp8(v8i a, v8i b) {
   const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+// A 32-byte fragment from two per-lane LDS bases plus a compile-time offset.
+template <int OFF>
+MOE_DEVICE v8i frag_at(const uint8_t* base0, const uint8_t* base1) {
+  const v4i x = *reinterpret_cast<const v4i*>(base0 + OFF);
+  const v4i y = *reinterpret_cast<const v4i*>(base1 + OFF);
+  return (v8i){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+// Barrier / counter waits as compiler-opaque memory clobbers, so that no LDS
+// access is moved across them and no fence forces a full vmcnt(0) drain.
+MOE_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+template <int N>
+MOE_DEVICE void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+MOE_DEVICE void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+MOE_DEVICE void dma16(const uint8_t* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 16, 0, 0);
+}
+MOE_DEVICE void dma4(const uint8_t* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 4, 0, 0);
 }
 
 template <int BM, bool FUSED>
@@ -102,9 +152,6 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
 void grouped_gemm_kernel(GemmArgs g) {
   using T = Tile<BM>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* smA = smem;
-  uint8_t* smB = smem + T::OFF_B;
-  float* smSA = reinterpret_cast<float*>(smem + T::OFF_SA);
   float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);
   float* smRed = reinterpret_cast<float*>(smem + T::OFF_RED);
 
@@ -114,21 +161,53 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int wm = wave / T::WN;
   const int wn = wave % T::WN;
 
-  // ---- XCD-aware tile mapping -------------------------------------------
-  const int64_t pid = blockIdx.x;
-  const int64_t xcd = pid % kXcds;
-  const int64_t li = pid / kXcds;
-  const int64_t per_group = (int64_t)kGroupM * g.n_tiles;
-  const int64_t mgl = li / per_group;
-  const int64_t within = li % per_group;
-  const int64_t j = within / kGroupM;
-  const int64_t b = (mgl * kXcds + xcd) * kGroupM + within % kGroupM;
-  if (b >= g.max_blocks) return;
+  // ---- expert-aligned, XCD-aware tile mapping ----------------------------
+  // Tiles are ordered run-major: for each run of consecutive blocks with the
+  // same expert (blocks [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT),
+  // n-tile major and block minor, so the n blocks that read one weight tile
+  // are adjacent.  Workgroup ids are dealt round-robin to the XCDs; XCD x
+  // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
+  // the same time on one XCD and fetch the weight tile from HBM once.
   const int ntpp = *g.ntpp;
-  if (b * BM >= ntpp) return;
-  const int e = g.eids[b];
+  const int64_t n_blocks = ntpp / BM;
+  const int64_t total = n_blocks * g.n_tiles;
+  const int64_t per_xcd = (total + kXcds - 1) / kXcds;
+  const int64_t pid = blockIdx.x;
+  const int64_t local = pid / kXcds;
+  if (local >= per_xcd) return;
+  const int64_t t = (pid % kXcds) * per_xcd + local;
+  if (t >= total) return;
+  const int64_t bq = t / g.n_tiles;  // a block of the tile's run
+  const int e = g.eids[bq];
+  int64_t back = 0, fwd = 0;
+  {
+    const int ln = threadIdx.x & 63;
+    for (int64_t base = bq - 1;; base -= 64) {  // blocks before bq with the same expert
+      const int64_t idx = base - ln;
+      const uint64_t end = __ballot(!(idx >= 0 && g.eids[idx] == e));
+      if (end) {
+        back += __ffsll((unsigned long long)end) - 1;
+        break;
+      }
+      back += 64;
+    }
+    for (int64_t base = bq + 1;; base += 64) {  // and after it
+      const int64_t idx = base + ln;
+      const uint64_t end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
+      if (end) {
+        fwd += __ffsll((unsigned long long)end) - 1;
+        break;
+      }
+      fwd += 64;
+    }
+  }
+  const int64_t b0 = bq - back;
+  const int64_t run = back + 1 + fwd;
+  const int64_t in_run = t - b0 * g.n_tiles;
+  const int64_t j = in_run / run;
+  const int64_t b = b0 + in_run % run;
   const int64_t K = g.K;
-  const int64_t KB = K / 128;
+  const int KB = (int)(K / 128);
   const int64_t NBt = g.N / 128;
   int64_t g0, g1;
   bool g1_store = true;
@@ -147,11 +226,9 @@ void grouped_gemm_kernel(GemmArgs g) {
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
     if (FUSED) {
-      const int64_t hcols = g.I;
       for (int ci = tid; ci < BM * 8; ci += kGemmThreads) {
         const int row = ci >> 3, cc = ci & 7;
-        *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * hcols + j * 128 + cc * 16) =
-            (v4i){0, 0, 0, 0};
+        *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
       }
       for (int row = tid; row < BM; row += kGemmThreads)
         g.hs[(b * BM + row) * (g.I / 128) + j] = kScaleFloor;
@@ -160,88 +237,80 @@ void grouped_gemm_kernel(GemmArgs g) {
         const int row = ci >> 5, cc = ci & 31;
         const int64_t slot = g.sorted[b * BM + row];
         if (slot >= g.S) continue;
-        const int grp = (cc * 8) >> 7;
+        const int grp = cc >> 4;
         if (grp == 1 && !g1_store) continue;
-        const int64_t n = (grp ? g1 : g0) * 128 + ((cc * 8) & 127);
+        const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
         *reinterpret_cast<v4i*>(g.C + slot * g.N + n) = (v4i){0, 0, 0, 0};
       }
     }
     return;
   }
 
-  // ---- per-thread global source pointers ---------------------------------
-  const uint8_t* a_src[T::A_PER_THREAD];
-  int a_dst[T::A_PER_THREAD];
-#pragma unroll
-  for (int i = 0; i < T::A_PER_THREAD; ++i) {
-    const int ci = tid + i * kGemmThreads;
-    const int row = (ci < T::A_CHUNKS) ? (ci >> 3) : 0;
-    const int cc = ci & 7;
+  auto a_row_of = [&](int row) -> int64_t {
     const int64_t pos = b * BM + row;
-    int64_t arow;
-    if (g.a_by_pos) {
-      arow = pos;
-    } else {
-      const int64_t slot = g.sorted[pos];
-      arow = (slot < g.S) ? slot / g.top_k : 0;
-    }
-    a_src[i] = g.A + arow * K + cc * 16;
-    a_dst[i] = row * 128 + ((cc ^ swz(row)) << 4);
-  }
-  const float* sa_src = g.As;
-  if (tid < BM) {
-    const int64_t pos = b * BM + tid;
-    int64_t arow;
-    if (g.a_by_pos) {
-      arow = pos;
-    } else {
-      const int64_t slot = g.sorted[pos];
-      arow = (slot < g.S) ? slot / g.top_k : 0;
-    }
-    sa_src = g.As + arow * KB;
-  }
-  const float* sb_src = g.Bs + ((int64_t)e * NBt + (tid == 0 ? g0 : g1)) * KB;
-  // B rows: chunk ci = tid + i*256 -> row r = (tid>>3) + 32*i, col chunk tid&7.
-  const int b_row0 = tid >> 3;
-  const int b_cc = tid & 7;
-  const uint8_t* b_src0 = g.B + ((int64_t)e * g.N + g0 * 128 + b_row0) * K + b_cc * 16;
-  const uint8_t* b_src1 = g.B + ((int64_t)e * g.N + g1 * 128 + b_row0) * K + b_cc * 16;
-  int b_dst[T::B_PER_THREAD];
-#pragma unroll
-  for (int i = 0; i < T::B_PER_THREAD; ++i) {
-    const int r = b_row0 + 32 * i;
-    b_dst[i] = r * 128 + ((b_cc ^ swz(r)) << 4);
-  }
-
-  v4i ra[T::A_PER_THREAD];
-  v4i rb[T::B_PER_THREAD];
-  float rsa = 0.0f, rsb = 0.0f;
-
-  auto load_tile = [&](int64_t kk) {
-#pragma unroll
-    for (int i = 0; i < T::A_PER_THREAD; ++i)
-      if (tid + i * kGemmThreads < T::A_CHUNKS)
-        ra[i] = *reinterpret_cast<const v4i*>(a_src[i] + kk * 128);
-#pragma unroll
-    for (int i = 0; i < T::B_PER_THREAD; ++i) {
-      const uint8_t* src = (i < 4) ? b_src0 + (int64_t)(32 * i) * K
-                                   : b_src1 + (int64_t)(32 * (i - 4)) * K;
-      rb[i] = *reinterpret_cast<const v4i*>(src + kk * 128);
-    }
-    if (tid < BM) rsa = sa_src[kk];
-    if (tid < 2) rsb = sb_src[kk];
+    if (g.a_by_pos) return pos;
+    const int64_t slot = g.sorted[pos];
+    return (slot < g.S) ? slot / g.top_k : 0;
   };
-  auto store_tile = [&](int buf) {
-    uint8_t* dA = smA + buf * T::A_BYTES;
-    uint8_t* dB = smB + buf * T::B_BYTES;
+
+  // Rows of this block that hold real slots (a prefix: padding follows them).
+  const int nvalid = __syncthreads_count(tid < BM && g.sorted[b * BM + (tid < BM ? tid : 0)] < g.S);
+
+  // ---- per-lane DMA offsets (32-bit, relative to uniform bases) ----------
+  // A instruction gi = wave + 4*i covers tile rows 8*gi .. 8*gi+7; lane L fills
+  // LDS slot L&7 of row R = 8*gi + L/8 with logical chunk slot_of(L&7, R).
+  uint32_t a_off[T::NA_W > 0 ? T::NA_W : 1];
 #pragma unroll
-    for (int i = 0; i < T::A_PER_THREAD; ++i)
-      if (tid + i * kGemmThreads < T::A_CHUNKS) *reinterpret_cast<v4i*>(dA + a_dst[i]) = ra[i];
+  for (int i = 0; i < T::NA_W; ++i) {
+    const int gi = wave + 4 * i;
+    const int row = (gi < T::NA) ? 8 * gi + (lane >> 3) : 0;
+    const int cc = slot_of(lane & 7, row);
+    a_off[i] = (uint32_t)(a_row_of(row) * K) + (uint32_t)(cc * 16);
+  }
+  // B instruction gi = wave + 4*i (i < 8) covers B-tile rows 8*gi .. 8*gi+7;
+  // tile rows 0..127 are scale group g0, rows 128..255 group g1.  The lane's
+  // row inside its group is 8*wave + 32*(i%4) + L/8, and its rotation does not
+  // depend on i (32*i leaves row mod 16 and bit 3 unchanged), so one lane
+  // offset serves all eight instructions; the rest is a uniform base.
+  uint32_t b_off;
+  {
+    const int r0 = 8 * wave + (lane >> 3);
+    const int cc = slot_of(lane & 7, r0);
+    b_off = (uint32_t)(r0 * K) + (uint32_t)(cc * 16);
+  }
+  // A scales: instruction s (issued by wave 3-s) covers rows 64*s .. 64*s+63.
+  const int s_idx = 3 - wave;
+  uint32_t sa_off = 0;
+  if (s_idx < T::NS) {
+    const int row = 64 * s_idx + lane;
+    sa_off = (uint32_t)(a_row_of(row < BM ? row : 0) * KB) * 4u;
+  }
+  const uint8_t* b_grp0 = g.B + ((int64_t)e * g.N + g0 * 128) * K;
+  const uint8_t* b_grp1 = g.B + ((int64_t)e * g.N + g1 * 128) * K;
+
+  auto issue_stage = [&](int kk, int stage) {
+    uint8_t* dst = smem + stage * T::STAGE;
+    const uint8_t* abase = g.A + kk * 128;
 #pragma unroll
-    for (int i = 0; i < T::B_PER_THREAD; ++i) *reinterpret_cast<v4i*>(dB + b_dst[i]) = rb[i];
-    if (tid < BM) smSA[buf * BM + tid] = rsa;
-    if (tid < 2) smSB[buf * 2 + tid] = rsb;
+    for (int i = 0; i < T::NA_W; ++i) {
+      const int gi = wave + 4 * i;
+      if (gi < T::NA) dma16(abase + a_off[i], dst + gi * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint8_t* bbase = (i < 4 ? b_grp0 : b_grp1) + (int64_t)(32 * (i & 3)) * K + kk * 128;
+      dma16(bbase + b_off, dst + T::A_BYTES + (wave + 4 * i) * 1024);
+    }
+    if (s_idx < T::NS)
+      dma4(reinterpret_cast<const uint8_t*>(g.As + kk) + sa_off,
+           smem + T::OFF_SA + stage * T::NS * 256 + s_idx * 256);
   };
+
+  // Weight scales of both groups for every K block (read once, plain loads).
+  for (int i = tid; i < 2 * KB; i += kGemmThreads) {
+    const int grp = i / KB, kk = i % KB;
+    smSB[grp * kMaxKB + kk] = g.Bs[((int64_t)e * NBt + (grp ? g1 : g0)) * KB + kk];
+  }
 
   v4f acc[T::RS][2][T::CS];
 #pragma unroll
@@ -253,53 +322,114 @@ void grouped_gemm_kernel(GemmArgs g) {
 
   const int row_base = wm * T::RS * 16;
   const int col_base = wn * T::CS * 16;
-  const int frag_row = lane & 15;
+  const int fr = lane & 15;
   const int kseg = lane >> 4;
+  // Per-lane fragment byte offsets within a stage (chunk h of the lane's 32 B).
+  const int lane0 = fr * 128 + (slot_of(2 * kseg, fr) << 4);
+  const int lane1 = fr * 128 + (slot_of(2 * kseg + 1, fr) << 4);
+  const int a_lane0 = row_base * 128 + lane0, a_lane1 = row_base * 128 + lane1;
+  const int b_lane0 = T::A_BYTES + col_base * 128 + lane0;
+  const int b_lane1 = T::A_BYTES + col_base * 128 + lane1;
+  const float* smSA = reinterpret_cast<const float*>(smem + T::OFF_SA);
+  const int sa_lane = row_base + 4 * kseg;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int64_t kk = 0; kk < KB; ++kk) {
-    const int cur = (int)(kk & 1);
-    if (kk + 1 < KB) load_tile(kk + 1);
-    const uint8_t* tA = smA + cur * T::A_BYTES;
-    const uint8_t* tB = smB + cur * T::B_BYTES;
-    v8i af[T::RS];
-    float sab[T::RS][2][4];
-    const float sb0 = smSB[cur * 2 + 0];
-    const float sb1 = smSB[cur * 2 + 1];
+  issue_stage(0, 0);
+  if (KB > 1) issue_stage(1, 1);
+  wait_lgkm0();  // the weight-scale ds_writes above
+
+  int ra = (nvalid - row_base + 15) / 16;
+  ra = ra < 0 ? 0 : (ra > T::RS ? T::RS : ra);
+
+  auto kloop = [&](auto ra_c) {
+    constexpr int RA = decltype(ra_c)::value;  // active 16-row subtiles of this wave
+    int stage = 0;
+    for (int kk = 0; kk < KB; ++kk) {
+      if (kk + 1 < KB) wait_vmcnt<T::VM>(); else wait_vmcnt<0>();
+      block_barrier();
+      if (kk + 2 < KB) issue_stage(kk + 2, stage == 0 ? 2 : stage - 1);
+      if constexpr (RA > 0) {
+        const uint8_t* st = smem + stage * T::STAGE;
+        const uint8_t* pa0 = st + a_lane0;
+        const uint8_t* pa1 = st + a_lane1;
+        const uint8_t* pb0 = st + b_lane0;
+        const uint8_t* pb1 = st + b_lane1;
+        const float* tSA = smSA + stage * T::NS * 64 + sa_lane;
+        v8i af[RA];
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+          ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
+        }(std::make_integer_sequence<int, RA>{});
+        // Column fragments double-buffered; MFMA t is issued before the scale
+        // FMAs of MFMA t-1, whose result is ready by then.  The per-row scale
+        // products a_s*b_s are formed per group; the one MFMA still pending at
+        // the group switch keeps its old products in sab_prev.
+        constexpr int NQ = 2 * T::CS;  // column fragments per step
+        constexpr int NT = NQ * RA;
+        v8i bq[2];
+        v4f p[2];
+        float sab[RA][4];
+        float sab_prev[4];
+        bq[0] = frag_at<0>(pb0, pb1);
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+          (
+              [&] {
+                constexpr int gg = Q / T::CS, c = Q % T::CS;
+                if constexpr (c == 0) {
+                  if constexpr (gg == 1) {
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r) {
-      af[r] = lds_frag(tA, row_base + r * 16 + frag_row, kseg);
-      const v4f sa4 =
-          *reinterpret_cast<const v4f*>(smSA + cur * BM + row_base + r * 16 + 4 * kseg);
+                    for (int v = 0; v < 4; ++v) sab_prev[v] = sab[RA - 1][v];
+                  }
+                  const float sb = smSB[gg * kMaxKB + kk];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        sab[r][0][v] = sa4[v] * sb0;
-        sab[r][1][v] = sa4[v] * sb1;
-      }
-    }
+                  for (int r = 0; r < RA; ++r) {
+                    const v4f sa4 = *reinterpret_cast<const v4f*>(tSA + r * 16);
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
+                    for (int v = 0; v < 4; ++v) sab[r][v] = sa4[v] * sb;
+                  }
+                }
+                if constexpr (Q + 1 < NQ) {
+                  constexpr int gn = (Q + 1) / T::CS, cn = (Q + 1) % T::CS;
+                  bq[(Q + 1) & 1] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
+                }
 #pragma unroll
-      for (int c = 0; c < T::CS; ++c) {
-        const v8i bf = lds_frag(tB, gg * 128 + col_base + c * 16 + frag_row, kseg);
+                for (int r = 0; r < RA; ++r) {
+                  const int t = Q * RA + r;
+                  p[t & 1] = mfma_fp8(af[r], bq[Q & 1]);
+                  if (t >= 1) {
+                    const int u = t - 1, uq = u / RA, ur = u % RA;
+                    const int ug = uq / T::CS, uc = uq % T::CS;
 #pragma unroll
-        for (int r = 0; r < T::RS; ++r) {
-          const v4f p = mfma_fp8(af[r], bf);
+                    for (int v = 0; v < 4; ++v) {
+                      const float sc = (ug == gg) ? sab[ur][v] : sab_prev[v];
+                      acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sc, acc[ur][ug][uc][v]);
+                    }
+                  }
+                }
+              }(),
+              ...);
+        }(std::make_integer_sequence<int, NQ>{});
+        {  // drain the last MFMA
+          constexpr int u = NT - 1, uq = u / RA, ur = u % RA;
+          constexpr int ug = uq / T::CS, uc = uq % T::CS;
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            acc[r][gg][c][v] = __builtin_fmaf(p[v], sab[r][gg][v], acc[r][gg][c][v]);
+            acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sab[ur][v], acc[ur][ug][uc][v]);
         }
       }
+      stage = (stage == 2) ? 0 : stage + 1;
     }
-    if (kk + 1 < KB) store_tile(cur ^ 1);
-    __syncthreads();
+  };
+  switch (ra) {
+    case 0: kloop(std::integral_constant<int, 0>{}); break;
+    case 1: if constexpr (T::RS >= 1) kloop(std::integral_constant<int, (T::RS >= 1 ? 1 : 0)>{}); break;
+    case 2: if constexpr (T::RS >= 2) kloop(std::integral_constant<int, (T::RS >= 2 ? 2 : 0)>{}); break;
+    case 3: if constexpr (T::RS >= 3) kloop(std::integral_constant<int, (T::RS >= 3 ? 3 : 0)>{}); break;
+    default: if constexpr (T::RS >= 4) kloop(std::integral_constant<int, (T::RS >= 4 ? 4 : 0)>{}); break;
   }
+  block_barrier();  // every wave is done with the ring; reuse it for staging
 
   // ---- epilogues ----------------------------------------------------------
   // Output element (r, gg, c, v) of this lane: row = row_base + r*16 + 4*kseg + v,
-  // column (within group gg) = col_base + c*16 + frag_row.
+  // column (within group gg) = col_base + c*16 + fr.
   if constexpr (FUSED) {
     float pmax[T::RS][4];
 #pragma unroll
@@ -312,9 +442,8 @@ void grouped_gemm_kernel(GemmArgs g) {
       for (int c = 0; c < T::CS; ++c)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float cg = round_bf16(acc[r][0][c][v]);
-          const float cu = round_bf16(acc[r][1][c][v]);
-          const float h = round_bf16(cg / (1.0f + __expf(-cg)) * cu);
+          const uint32_t gu = pack_bf16x2(acc[r][0][c][v], acc[r][1][c][v]);
+          const float h = silu_mul_bf16(lo_bf16(gu), hi_bf16(gu));
           acc[r][0][c][v] = h;
           pmax[r][v] = fmaxf(pmax[r][v], fabsf(h));
         }
@@ -327,10 +456,10 @@ void grouped_gemm_kernel(GemmArgs g) {
         m = fmaxf(m, __shfl_xor(m, 2));
         m = fmaxf(m, __shfl_xor(m, 4));
         m = fmaxf(m, __shfl_xor(m, 8));
-        if (frag_row == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
+        if (fr == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
       }
     __syncthreads();
-    uint8_t* stage = smem;  // [BM][128] fp8 codes
+    uint8_t* stage_out = smem;  // [BM][128] fp8 codes
     const int64_t hgroups = g.I / 128;
 #pragma unroll
     for (int r = 0; r < T::RS; ++r)
@@ -342,25 +471,24 @@ void grouped_gemm_kernel(GemmArgs g) {
         for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
         const float sc = group_scale(amax);
         const float inv = 1.0f / sc;
-        if (wn == 0 && frag_row == 0) g.hs[(b * BM + row) * hgroups + j] = sc;
+        if (wn == 0 && fr == 0) g.hs[(b * BM + row) * hgroups + j] = sc;
 #pragma unroll
         for (int c = 0; c < T::CS; c += 2) {
-          // two columns per cvt; columns differ by 16 so write bytes separately
           const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
           const float q1 = clamp_fp8(div_by(acc[r][0][c + 1][v], sc, inv));
           const uint32_t pk = pack4_e4m3(q0, q1, 0.0f, 0.0f);
-          stage[row * 128 + col_base + c * 16 + frag_row] = (uint8_t)(pk & 0xFF);
-          stage[row * 128 + col_base + (c + 1) * 16 + frag_row] = (uint8_t)((pk >> 8) & 0xFF);
+          stage_out[row * 128 + col_base + c * 16 + fr] = (uint8_t)(pk & 0xFF);
+          stage_out[row * 128 + col_base + (c + 1) * 16 + fr] = (uint8_t)((pk >> 8) & 0xFF);
         }
       }
     __syncthreads();
     for (int ci = tid; ci < BM * 8; ci += kGemmThreads) {
       const int row = ci >> 3, cc = ci & 7;
       *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) =
-          *reinterpret_cast<const v4i*>(stage + row * 128 + cc * 16);
+          *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
     }
   } else {
-    uint16_t* stage = reinterpret_cast<uint16_t*>(smem);  // [BM][256] bf16
+    uint16_t* stage_out = reinterpret_cast<uint16_t*>(smem);  // [BM][256] bf16
 #pragma unroll
     for (int r = 0; r < T::RS; ++r)
 #pragma unroll
@@ -377,8 +505,8 @@ void grouped_gemm_kernel(GemmArgs g) {
           for (int c = 0; c < T::CS; ++c) {
             float val = acc[r][gg][c][v];
             if (g.topk_w) val = val * w;
-            stage[row * 256 + gg * 128 + col_base + c * 16 + frag_row] =
-                (uint16_t)f32_to_bf16_bits(val);
+            stage_out[row * 256 + gg * 128 + col_base + c * 16 + fr] =
+                (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
           }
       }
     __syncthreads();
@@ -390,7 +518,7 @@ void grouped_gemm_kernel(GemmArgs g) {
       if (grp == 1 && !g1_store) continue;
       const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
       *reinterpret_cast<v4i*>(g.C + slot * g.N + n) =
-          *reinterpret_cast<const v4i*>(stage + row * 256 + cc * 8);
+          *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
     }
   }
 }
@@ -401,13 +529,12 @@ static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)grouped_gemm_kernel<BM, FUSED>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            T::LDS_BYTES) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES) != hipSuccess)
       return kErrLaunch;
     attr_set = true;
   }
-  const int64_t n_groups = (args.max_blocks + kGroupM - 1) / kGroupM;
-  const int64_t grid = (n_groups + kXcds - 1) / kXcds * kXcds * kGroupM * args.n_tiles;
+  // Upper bound on the tile count (the real one depends on ntpp, on the device).
+  const int64_t grid = (args.max_blocks * args.n_tiles + kXcds - 1) / kXcds * kXcds;
   if (grid <= 0) return kOk;
   hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(kGemmThreads),
                      T::LDS_BYTES, st, args);
@@ -427,6 +554,12 @@ static int dispatch_gemm(int BM, const GemmArgs& args, hipStream_t st) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// 32-bit lane offsets: every A row and every expert's B block must be
+// addressable with a uint32 offset from its base.
+static bool offsets_fit(int64_t rows, int64_t N, int64_t K) {
+  return rows * K < (int64_t)1 << 32 && N * K < (int64_t)1 << 32;
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -438,7 +571,7 @@ extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void*
                                 int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
                                 int64_t max_padded, void* C, void* stream) {
   if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
-  if (N % 128 != 0 || K % 128 != 0) return kErrBadShape;
+  if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
   if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
@@ -446,6 +579,8 @@ extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void*
   if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
     return kErrNullPointer;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return kErrBadShape;
+  const int64_t a_rows = a_by_pos ? max_padded : (S + top_k - 1) / top_k;
+  if (!offsets_fit(a_rows, N, K)) return kErrBadShape;
   GemmArgs g{};
   g.A = (const uint8_t*)A;
   g.As = A_scale;
@@ -475,7 +610,7 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
                                        int32_t BM, int64_t max_padded, void* hq, float* hs,
                                        void* stream) {
   if (S < 0 || H <= 0 || I <= 0 || max_padded < 0) return kErrBadShape;
-  if (H % 128 != 0 || I % 128 != 0) return kErrBadShape;
+  if (H % 128 != 0 || I % 128 != 0 || H > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
   if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
@@ -483,6 +618,7 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
   if (!Aq || !A_scale || !W13 || !W13_scale || !sorted_ids || !expert_ids || !ntpp || !hq || !hs)
     return kErrNullPointer;
   if (!aligned16(Aq) || !aligned16(W13) || !aligned16(hq)) return kErrBadShape;
+  if (!offsets_fit((S + top_k - 1) / top_k, 2 * I, H)) return kErrBadShape;
   GemmArgs g{};
   g.A = (const uint8_t*)Aq;
   g.As = A_scale;
@@ -507,22 +643,22 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
 }
 
 // Layout probe: one wave computes C[16][16] = A[16][128] . B[16][128]^T through
-// the same fragment loader and MFMA call as the GEMM, reading A/B through LDS
-// with the GEMM's swizzle and writing C with the GEMM's output mapping.
+// the GEMM's LDS row swizzle, fragment loader, MFMA call and output mapping.
 __global__ void mfma_probe_kernel(const uint8_t* A, const uint8_t* B, float* C) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA[16 * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[16 * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t sAB[2 * 16 * 128];
   const int lane = threadIdx.x;
-  for (int ci = lane; ci < 128; ci += 64) {
-    const int row = ci >> 3, cc = ci & 7;
-    *reinterpret_cast<v4i*>(sA + row * 128 + ((cc ^ swz(row)) << 4)) =
-        *reinterpret_cast<const v4i*>(A + row * 128 + cc * 16);
-    *reinterpret_cast<v4i*>(sB + row * 128 + ((cc ^ swz(row)) << 4)) =
-        *reinterpret_cast<const v4i*>(B + row * 128 + cc * 16);
+  for (int ci = lane; ci < 256; ci += 64) {
+    const int row = (ci >> 3) & 15, cc = ci & 7;
+    const uint8_t* src = (ci < 128 ? A : B) + row * 128 + cc * 16;
+    *reinterpret_cast<v4i*>(sAB + (ci < 128 ? 0 : 2048) + row * 128 + (slot_of(cc, row) << 4)) =
+        *reinterpret_cast<const v4i*>(src);
   }
   __syncthreads();
-  const v4f p = mfma_fp8(lds_frag(sA, lane & 15, lane >> 4), lds_frag(sB, lane & 15, lane >> 4));
-  for (int v = 0; v < 4; ++v) C[(4 * (lane >> 4) + v) * 16 + (lane & 15)] = p[v];
+  const int fr = lane & 15, kseg = lane >> 4;
+  const uint8_t* p0 = sAB + fr * 128 + (slot_of(2 * kseg, fr) << 4);
+  const uint8_t* p1 = sAB + fr * 128 + (slot_of(2 * kseg + 1, fr) << 4);
+  const v4f p = mfma_fp8(frag_at<0>(p0, p1), frag_at<2048>(p0, p1));
+  for (int v = 0; v < 4; ++v) C[(4 * kseg + v) * 16 + fr] = p[v];
 }
 
 extern "C" int moe_debug_mfma_probe(const void* A, const void* B, float* C, void* stream) {
