@@ -86,7 +86,8 @@ struct Tile {
   static constexpr int OFF_SA = kStages * STAGE;
   static constexpr int OFF_SB = OFF_SA + kStages * NS * 256;
   static constexpr int OFF_RED = OFF_SB + 2 * kMaxKB * 4;
-  static constexpr int LDS_BYTES = OFF_RED + WN * BM * 4;
+  static constexpr int OFF_ROW = OFF_RED + WN * BM * 4;  // per-row slot id and routed weight
+  static constexpr int LDS_BYTES = OFF_ROW + BM * 8;
   static_assert(BM * 512 <= OFF_SA, "bf16 output staging must fit in the operand ring");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(VM < 16, "vmcnt immediate");
@@ -154,6 +155,8 @@ void grouped_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);
   float* smRed = reinterpret_cast<float*>(smem + T::OFF_RED);
+  int32_t* smSlot = reinterpret_cast<int32_t*>(smem + T::OFF_ROW);
+  float* smW = reinterpret_cast<float*>(smem + T::OFF_ROW + BM * 4);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -254,7 +257,16 @@ void grouped_gemm_kernel(GemmArgs g) {
   };
 
   // Rows of this block that hold real slots (a prefix: padding follows them).
-  const int nvalid = __syncthreads_count(tid < BM && g.sorted[b * BM + (tid < BM ? tid : 0)] < g.S);
+  // The block's slot ids (and routed weights) once, for the epilogue; the
+  // valid rows of the block are a prefix (padding follows them).
+  bool row_valid = false;
+  if (tid < BM) {
+    const int32_t slot = g.sorted[b * BM + tid];
+    row_valid = slot < g.S;
+    smSlot[tid] = slot;
+    if (!FUSED) smW[tid] = (g.topk_w && row_valid) ? g.topk_w[slot] : 1.0f;
+  }
+  const int nvalid = __syncthreads_count(row_valid);
 
   // ---- per-lane DMA offsets (32-bit, relative to uniform bases) ----------
   // A instruction gi = wave + 4*i covers tile rows 8*gi .. 8*gi+7; lane L fills
@@ -494,11 +506,7 @@ void grouped_gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = row_base + r * 16 + 4 * kseg + v;
-        float w = 1.0f;
-        if (g.topk_w) {
-          const int64_t slot = g.sorted[b * BM + row];
-          if (slot < g.S) w = g.topk_w[slot];
-        }
+        const float w = smW[row];
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
@@ -512,7 +520,7 @@ void grouped_gemm_kernel(GemmArgs g) {
     __syncthreads();
     for (int ci = tid; ci < BM * 32; ci += kGemmThreads) {
       const int row = ci >> 5, cc = ci & 31;
-      const int64_t slot = g.sorted[b * BM + row];
+      const int64_t slot = smSlot[row];
       if (slot >= g.S) continue;
       const int grp = cc >> 4;
       if (grp == 1 && !g1_store) continue;
