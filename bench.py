@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -45,6 +46,18 @@ def stage_bytes(wl, ntpp: int, active: int) -> dict[str, float]:
         "w2": w2 + S * I + 4 * S * I / 128 + 2 * S * H + 4 * S,
         "reduce": 2 * S * H + 2 * T * H,
     }
+
+
+def measured_traffic(workload: str, kernel: str) -> tuple[float | None, str | None]:
+    """HBM bytes per launch of ``kernel`` on ``workload`` as recorded by the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by the copy calibration)
+    in profiles/*_hbm_traffic.md; (None, None) if no summary holds it."""
+    pat = re.compile(r"traffic_bytes\[(\w+),\s*([^\]]+)\]\s*=\s*([0-9.eE+]+)")
+    for path in sorted((ROOT / "profiles").glob("*_hbm_traffic.md")):
+        for m in pat.finditer(path.read_text()):
+            if m.group(1) == workload and m.group(2).replace(" ", "") == kernel.replace(" ", ""):
+                return float(m.group(3)), path.name
+    return None, None
 
 
 def cpu_baseline(data, wl, budget_s: float) -> dict:
@@ -187,7 +200,9 @@ def main() -> int:
     else:
         roof = {"bound": "mfma", "achieved": w13_tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                 "frac": w13_tflops / PEAK_FP8_TFLOPS}
-    roof.update({"traffic": None, "kernel": "grouped_gemm_kernel<BM,true> (W13 + SiLU*up + 1x128 quant)",
+    traffic, traffic_src = measured_traffic(wl.name, f"grouped_gemm_kernel<{wl.block_m},true>")
+    roof.update({"traffic": traffic, "traffic_source": traffic_src,
+                 "kernel": f"grouped_gemm_kernel<{wl.block_m},true> (W13 + SiLU*up + 1x128 quant)",
                  "alg_bytes": sbytes["w13"], "alg_flop": flop_w13, "avg_us": stage_ms["w13"] * 1e3,
                  "mfma_frac": w13_tflops / PEAK_FP8_TFLOPS, "hbm_frac": w13_gbs / PEAK_HBM_GBS})
     result = {

@@ -10,8 +10,11 @@
  * the reference's in-repo decomposition (overlap/overlap_forward.py) and its
  * in-repo copy of the grouped-GEMM kernel (overlap/kernels.py).
  *
- * Pinning (what independent checks each function is held to) is listed in
- * oracle/README.md and exercised by tests/test_oracle_*.py.
+ * Pinning: every function is held by tests/test_oracle_*.py to checks that
+ * do not retype its formula -- torch's own float8 / bfloat16 casts over
+ * exhaustive or dense samples, the reference's own test cases restated as
+ * known answers, brute force on tiny inputs, closed forms and invariants --
+ * and by the committed fixtures under tests/golden/.
  */
 #include <math.h>
 #include <stdint.h>

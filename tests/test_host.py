@@ -1,0 +1,80 @@
+"""Host-side logic that runs without a GPU: the tile configuration heuristic
+(A4), the workload table, the bench contract's CPU parts."""
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_moe_config_block_m_tracks_rows_per_expert():
+    from td_benchmark_amd import ops
+
+    # DeepSeek-V3 prefill: 8192*8/256 = 256 rows per expert -> 128
+    assert ops.get_moe_config(8192, 256, 8)["BLOCK_SIZE_M"] == 128
+    # decode: 128*8/256 = 4 rows per expert -> 16
+    assert ops.get_moe_config(128, 256, 8)["BLOCK_SIZE_M"] == 16
+    assert ops.get_moe_config(64, 4, 2)["BLOCK_SIZE_M"] == 32   # 32 rows per expert
+    assert ops.get_moe_config(512, 64, 8)["BLOCK_SIZE_M"] == 64
+    for T in (1, 7, 100, 4096, 65536):
+        cfg = ops.get_moe_config(T, 128, 8)
+        assert cfg["BLOCK_SIZE_M"] in ops.SUPPORTED_BLOCK_M
+        assert cfg["BLOCK_SIZE_K"] == 128
+
+
+def test_workload_table_matches_benchmark_configs():
+    from td_benchmark_amd import workloads
+
+    c = workloads.CONFIGS
+    assert (c["dsv3"].T, c["dsv3"].H, c["dsv3"].I, c["dsv3"].E, c["dsv3"].top_k) == (8192, 7168, 2048, 256, 8)
+    assert (c["tiny"].T, c["tiny"].H, c["tiny"].I, c["tiny"].E, c["tiny"].top_k) == (64, 256, 512, 8, 2)
+    assert c["dsv3"].gemm_flop == 6 * 8192 * 8 * 7168 * 2048
+    for wl in c.values():
+        assert wl.H % 128 == 0 and wl.I % 128 == 0
+        assert wl.block_m in (16, 32, 64, 128)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout.strip() == ""
+
+
+def test_bench_stage_bytes_and_traffic_lookup():
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from td_benchmark_amd import workloads
+
+    wl = workloads.CONFIGS["dsv3"]
+    b = bench.stage_bytes(wl, ntpp=81024, active=256)
+    # W13 weights dominate: 256 experts x 2I x H bytes
+    assert b["w13"] > 256 * 2 * 2048 * 7168
+    assert b["reduce"] == 2 * wl.S * wl.H + 2 * wl.T * wl.H
+    traffic, src = bench.measured_traffic("dsv3", "grouped_gemm_kernel<128,true>")
+    if src is not None:
+        assert traffic > b["w13"] * 0.5
+    assert bench.measured_traffic("no_such_workload", "x") == (None, None)
+
+
+def test_bench_metric_is_baseline_metric():
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    base = json.loads((ROOT / "BASELINE.json").read_text())
+    assert bench.METRIC == base["metric"]
+
+
+def test_ops_fail_loudly_without_library(monkeypatch, tmp_path):
+    from td_benchmark_amd import _lib
+
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.lib()

@@ -1,0 +1,165 @@
+"""Pins the oracle's block-scaled FP8 grouped GEMM (A5/A8), silu_and_mul (A6)
+and top-k reduce (A9).
+
+The GEMM is checked against a float64 numpy matmul of the dequantised operands
+(codes decoded by torch's float8 cast, scales broadcast per 128x128 block), a
+computation that shares no code with the C loop: E=1/top-1 against a dense
+product (the reference's tests/test_golden.py:9-26 case), multi-expert routing
+slot by slot, routed weights, rows addressed by position, expert -1 blocks and
+masked padding rows.  The test also shows that it would catch a transposed
+weight scale index or a missing routed weight.  A6 and A9 are checked against
+torch's silu and an fp32 sum.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+
+def decode(codes: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(codes)).view(torch.float8_e4m3fn).double().numpy()
+
+
+def deq_rows(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """[R,K] codes with [R,K/128] scales -> float64."""
+    return decode(q) * np.repeat(s.astype(np.float64), 128, axis=1)[:, :q.shape[1]]
+
+
+def deq_weights(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """[E,N,K] codes with [E,N/128,K/128] scales -> float64."""
+    sc = np.repeat(np.repeat(s.astype(np.float64), 128, axis=1), 128, axis=2)
+    return decode(q) * sc[:, :q.shape[1], :q.shape[2]]
+
+
+def rand_operands(rng, rows, E, N, K):
+    a = rng.standard_normal((rows, K)).astype(np.float32)
+    q_a, s_a = oracle.quant_group128(oracle.f32_to_bf16(a))
+    w = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
+    # make the weight scales differ strongly between blocks so that a wrong
+    # scale index changes the result
+    w *= np.exp2(rng.integers(-3, 4, (E, (N + 127) // 128, (K + 127) // 128))).repeat(128, 1).repeat(128, 2)[:, :N, :K]
+    q_w, s_w = oracle.quant_block128(w)
+    return q_a, s_a, q_w, s_w
+
+
+def within(got_bits: np.ndarray, exact: np.ndarray, l1: np.ndarray) -> np.ndarray:
+    """bf16 result within half an ulp-ish of the exact value plus fp32 chain error."""
+    got = oracle.bf16_to_f32(got_bits).astype(np.float64)
+    return np.abs(got - exact) <= 2.0 ** -8 * np.abs(exact) + 2.0 ** -20 * l1 + 1e-30
+
+
+def test_gemm_e1_top1_equals_dense_product():
+    rng = np.random.default_rng(0)
+    T, N, K = 24, 384, 256
+    q_a, s_a, q_w, s_w = rand_operands(rng, T, 1, N, K)
+    ids = np.zeros(T, np.int32)
+    sorted_ids, eids, ntpp = oracle.moe_align(ids, 1, 16)
+    got = oracle.grouped_gemm(q_a, s_a, q_w, s_w, sorted_ids, eids, ntpp, 16, T, 1)
+    A, B = deq_rows(q_a, s_a), deq_weights(q_w, s_w)[0]
+    exact = A @ B.T
+    l1 = np.abs(A) @ np.abs(B).T
+    assert np.all(within(got, exact, l1))
+    # a wrong block-scale index (n or k block order mixed up) would be caught
+    for s_wrong in (s_w[:, ::-1, :], s_w[:, :, ::-1]):
+        wrong = A @ deq_weights(q_w, np.ascontiguousarray(s_wrong))[0].T
+        assert not np.all(within(got, wrong, l1))
+    # and so would a missing activation scale
+    assert not np.all(within(got, decode(q_a) @ B.T, l1))
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_gemm_multi_expert_slot_by_slot(routed):
+    rng = np.random.default_rng(1)
+    T, k, E, N, K, BM = 30, 2, 5, 256, 384, 8
+    q_a, s_a, q_w, s_w = rand_operands(rng, T, E, N, K)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[3, 1] = -1                       # a slot that is not local: never written
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    S = T * k
+    sorted_ids, eids, ntpp = oracle.moe_align(ids.ravel(), E, BM)
+    got = oracle.grouped_gemm(q_a, s_a, q_w, s_w, sorted_ids, eids, ntpp, BM, S, k,
+                              topk_w=w.ravel() if routed else None)
+    A, B = deq_rows(q_a, s_a), deq_weights(q_w, s_w)
+    for s in range(S):
+        t, e = s // k, ids.ravel()[s]
+        if e < 0:
+            assert np.all(got[s] == 0)
+            continue
+        exact = B[e] @ A[t]
+        l1 = np.abs(B[e]) @ np.abs(A[t])
+        if routed:
+            exact = exact * np.float64(w.ravel()[s])
+            l1 = l1 * w.ravel()[s]
+        assert np.all(within(got[s], exact, l1)), s
+    if routed:
+        # dropping the routed weight would be caught
+        s0 = int(np.nonzero(ids.ravel() >= 0)[0][0])
+        e0 = ids.ravel()[s0]
+        unweighted = B[e0] @ A[s0 // k]
+        assert not np.all(within(got[s0], unweighted, np.abs(B[e0]) @ np.abs(A[s0 // k])))
+
+
+def test_gemm_rows_by_position_and_expert_minus_one_blocks():
+    rng = np.random.default_rng(2)
+    T, k, E, N, K, BM = 12, 2, 3, 128, 256, 4
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    S = T * k
+    sorted_ids, eids, ntpp = oracle.moe_align(ids.ravel(), E, BM)
+    q_a, s_a, q_w, s_w = rand_operands(rng, sorted_ids.size, E, N, K)   # A indexed by position
+    eids_masked = eids.copy()
+    eids_masked[1] = -1                                                  # block 1 not local
+    got = oracle.grouped_gemm(q_a, s_a, q_w, s_w, sorted_ids, eids_masked, ntpp, BM, S, k,
+                              a_row_by_pos=True)
+    A, B = deq_rows(q_a, s_a), deq_weights(q_w, s_w)
+    for p in range(ntpp):
+        s = sorted_ids[p]
+        if s >= S:
+            continue
+        if p // BM == 1:
+            assert np.all(got[s] == 0)
+            continue
+        e = eids[p // BM]
+        assert np.all(within(got[s], B[e] @ A[p], np.abs(B[e]) @ np.abs(A[p])))
+
+
+def test_gemm_magnitude_bounds_result():
+    rng = np.random.default_rng(3)
+    T, N, K = 8, 128, 256
+    q_a, s_a, q_w, s_w = rand_operands(rng, T, 1, N, K)
+    sorted_ids, eids, ntpp = oracle.moe_align(np.zeros(T, np.int32), 1, 16)
+    out, mag = oracle.grouped_gemm(q_a, s_a, q_w, s_w, sorted_ids, eids, ntpp, 16, T, 1,
+                                   with_magnitude=True)
+    A, B = deq_rows(q_a, s_a), deq_weights(q_w, s_w)[0]
+    np.testing.assert_allclose(mag, np.abs(A) @ np.abs(B).T, rtol=1e-5)
+    assert np.all(np.abs(oracle.bf16_to_f32(out)) <= mag * (1 + 2 ** -7))
+
+
+def test_silu_and_mul_matches_torch_silu():
+    rng = np.random.default_rng(4)
+    R, I = 64, 512
+    c = oracle.f32_to_bf16((rng.standard_normal((R, 2 * I)) * 4).astype(np.float32))
+    got = oracle.silu_and_mul(c)
+    ct = torch.from_numpy(c.view(np.int16)).view(torch.bfloat16).float()
+    ref = (torch.nn.functional.silu(ct[:, :I]) * ct[:, I:]).to(torch.bfloat16)
+    ref = ref.view(torch.int16).numpy().view(np.uint16)
+    diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    # silu's fp32 evaluation order may differ from torch's by an fp32 ulp, which
+    # can move a bf16 rounding decision by one ulp on rare ties
+    assert diff.max() <= 1
+    assert np.mean(diff > 0) < 1e-3
+
+
+def test_reduce_is_fp32_sum_rounded_once():
+    rng = np.random.default_rng(5)
+    T, k, H = 16, 8, 256
+    D = oracle.f32_to_bf16(rng.standard_normal((T * k, H)).astype(np.float32))
+    got = oracle.moe_reduce(D, T, k)
+    Df = oracle.bf16_to_f32(D).reshape(T, k, H)
+    acc = np.zeros((T, H), np.float32)
+    for i in range(k):
+        acc = acc + Df[:, i]
+    ref = torch.from_numpy(acc).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
