@@ -82,6 +82,19 @@ int moe_grouped_gemm(const void* A, const float* A_scale, const void* B, const f
                      int64_t N, int64_t K, int32_t E, int32_t block_size_m, int64_t max_padded,
                      void* C, void* stream);
 
+/* A5 / A8 with an explicit workgroup -> tile order (the knob the reference's
+ * tile-order sweep varies, microbench/mb_tile_order_groupgemm.py:13):
+ * 0 expert-major, XCD-contiguous (what moe_grouped_gemm uses); 1 shuffled
+ * (a fixed bijective scramble of the expert-major order); 2 half-phase (the
+ * first and second halves of the expert-major order interleaved).  Results
+ * are identical for every order. */
+int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
+                             const float* B_scale, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* ntpp,
+                             const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
+                             int64_t N, int64_t K, int32_t E, int32_t block_size_m,
+                             int64_t max_padded, int32_t tile_order, void* C, void* stream);
+
 /* A5 + A6 + A7 fused -- W13 grouped GEMM with SiLU*up and 1x128 FP8 quant of
  * the intermediate in the epilogue.
  * Replaces the sequence dispatch_fused_moe_kernel(W13, mul_routed_weight=False,
@@ -102,11 +115,28 @@ int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W1
  * c [R, 2I] bf16 -> h [R, I] bf16; I % 8 == 0. */
 int moe_silu_and_mul(const void* c_bf16, int64_t R, int64_t I, void* h_bf16, void* stream);
 
+/* A6 + A7 standalone -- SiLU*up then 1x128 FP8 quant of the bf16 product, one
+ * pass: replaces silu_and_mul followed by moe_kernel_quantize_input
+ * (overlap/overlap_forward.py:277-284) where C13 exists (the unfused chain;
+ * the reference's swiglu_group128 kernel, tdx/kernels/swiglu_quantize_fp8.py:
+ * 80-85, microbench/mb_quant_kernels.py:11).  Codes and scales equal those of
+ * moe_silu_and_mul followed by moe_quant_group128 bit for bit.
+ * c [R, 2I] bf16 -> q [R, I] e4m3fn, scales [R, I/128]; I % 128 == 0. */
+int moe_silu_mul_quant_group128(const void* c_bf16, int64_t R, int64_t I, void* q_fp8,
+                                float* scales, void* stream);
+
 /* A9 -- top-k un-permute / reduce.  Replaces torch.sum(C_down.view(T,k,H),
  * dim=1) (overlap/overlap_forward.py:304-313): y[t] = bf16(sum_i D[t*k+i]),
  * fp32 accumulation.  D [T*k, H] bf16 -> y [T, H] bf16; H % 8 == 0, k <= 32. */
 int moe_reduce_topk(const void* D_bf16, int64_t T, int32_t top_k, int64_t H, void* y_bf16,
                     void* stream);
+
+/* A9 + shared expert -- the reduce followed by the bf16 add of the shared
+ * expert's output: y[t] = bf16(bf16(sum_i D[t*k+i]) + addend[t]), replacing
+ * `result + shared(hidden)` (schemes/vllm_tp.py:62-63, schemes/vllm_ep.py:
+ * 66-67) without re-reading the [T,H] sum.  addend [T, H] bf16. */
+int moe_reduce_topk_add(const void* D_bf16, const void* addend_bf16, int64_t T, int32_t top_k,
+                        int64_t H, void* y_bf16, void* stream);
 
 /* Test hook (no reference counterpart): one 16x16x128 FP8 MFMA through the
  * GEMM's own LDS swizzle, fragment loader and output mapping.

@@ -17,8 +17,13 @@ namespace moe {
 
 constexpr int kMaxTopK = 32;
 
-template <int KMAX>
+// ADD: y[t] = bf16( float(bf16(sum)) + float(addend[t]) ), the bf16 sum of the
+// routed output and the shared expert's output (result + shared(hidden) of
+// schemes/vllm_tp.py:62-63 and schemes/vllm_ep.py:66-67), fused into the
+// reduce so the [T,H] sum is not re-read.
+template <int KMAX, bool ADD>
 __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __restrict__ D,
+                                                          const uint16_t* __restrict__ addend,
                                                           uint16_t* __restrict__ y, int64_t T,
                                                           int k, int64_t chunks_per_row) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -30,6 +35,8 @@ __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __rest
 #pragma unroll
   for (int i = 0; i < KMAX; ++i)
     if (i < k) rows[i] = *reinterpret_cast<const v4i*>(D + (t * k + i) * H + cc * 8);
+  v4i add = {0, 0, 0, 0};
+  if constexpr (ADD) add = *reinterpret_cast<const v4i*>(addend + t * H + cc * 8);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
@@ -44,8 +51,15 @@ __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __rest
   }
   v4i out;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    out[j] = (int)(f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16));
+  for (int j = 0; j < 4; ++j) {
+    uint32_t lo = f32_to_bf16_bits(acc[2 * j]), hi = f32_to_bf16_bits(acc[2 * j + 1]);
+    if constexpr (ADD) {
+      const uint32_t a = (uint32_t)add[j];
+      lo = f32_to_bf16_bits(bf16_to_f32(lo) + lo_bf16(a));
+      hi = f32_to_bf16_bits(bf16_to_f32(hi) + hi_bf16(a));
+    }
+    out[j] = (int)(lo | (hi << 16));
+  }
   *reinterpret_cast<v4i*>(y + t * H + cc * 8) = out;
 }
 
@@ -69,7 +83,39 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __res
   *reinterpret_cast<v4i*>(h + r * I + cc * 8) = out;
 }
 
-static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }  // null passes
+
+
+
+static int launch_reduce(const void* D_bf16, const void* addend, int64_t T, int32_t top_k,
+                         int64_t H, void* y, void* stream) {
+  if (T < 0 || H < 0) return kErrBadShape;
+  if (top_k <= 0 || top_k > kMaxTopK) return kErrBadTopK;
+  if (T == 0 || H == 0) return kOk;
+  if (!D_bf16 || !y) return kErrNullPointer;
+  if (H % 8 != 0 || !aligned16(D_bf16) || !aligned16(y) || !aligned16(addend)) return kErrBadShape;
+  const int64_t cpr = H / 8;
+  const int64_t blocks = (T * cpr + 255) / 256;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* d = (const uint16_t*)D_bf16;
+  const uint16_t* a = (const uint16_t*)addend;
+  uint16_t* out = (uint16_t*)y;
+  const dim3 grid((unsigned)blocks);
+  if (top_k <= 8) {
+    if (a)
+      hipLaunchKernelGGL((reduce_topk_kernel<8, true>), grid, dim3(256), 0, st, d, a, out, T, (int)top_k, cpr);
+    else
+      hipLaunchKernelGGL((reduce_topk_kernel<8, false>), grid, dim3(256), 0, st, d, a, out, T, (int)top_k, cpr);
+  } else {
+    if (a)
+      hipLaunchKernelGGL((reduce_topk_kernel<kMaxTopK, true>), grid, dim3(256), 0, st, d, a, out, T,
+                         (int)top_k, cpr);
+    else
+      hipLaunchKernelGGL((reduce_topk_kernel<kMaxTopK, false>), grid, dim3(256), 0, st, d, a, out, T,
+                         (int)top_k, cpr);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
 
 }  // namespace moe
 
@@ -77,22 +123,13 @@ using namespace moe;
 
 extern "C" int moe_reduce_topk(const void* D_bf16, int64_t T, int32_t top_k, int64_t H, void* y,
                                void* stream) {
-  if (T < 0 || H < 0) return kErrBadShape;
-  if (top_k <= 0 || top_k > kMaxTopK) return kErrBadTopK;
-  if (T == 0 || H == 0) return kOk;
-  if (!D_bf16 || !y) return kErrNullPointer;
-  if (H % 8 != 0 || !aligned16(D_bf16) || !aligned16(y)) return kErrBadShape;
-  const int64_t cpr = H / 8;
-  const int64_t blocks = (T * cpr + 255) / 256;
-  hipStream_t st = (hipStream_t)stream;
-  if (top_k <= 8) {
-    hipLaunchKernelGGL(reduce_topk_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint16_t*)D_bf16, (uint16_t*)y, T, (int)top_k, cpr);
-  } else {
-    hipLaunchKernelGGL(reduce_topk_kernel<kMaxTopK>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint16_t*)D_bf16, (uint16_t*)y, T, (int)top_k, cpr);
-  }
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  return launch_reduce(D_bf16, nullptr, T, top_k, H, y, stream);
+}
+
+extern "C" int moe_reduce_topk_add(const void* D_bf16, const void* addend_bf16, int64_t T,
+                                   int32_t top_k, int64_t H, void* y, void* stream) {
+  if (T > 0 && H > 0 && !addend_bf16) return kErrNullPointer;
+  return launch_reduce(D_bf16, addend_bf16, T, top_k, H, y, stream);
 }
 
 extern "C" int moe_silu_and_mul(const void* c_bf16, int64_t R, int64_t I, void* h_bf16,

@@ -114,6 +114,7 @@ struct GemmArgs {
   int top_k;
   int a_by_pos;
   int E;
+  int tile_order;          // 0 expert-major (XCD-contiguous), 1 shuffled, 2 half-phase
 };
 
 // Chunk swizzle of an LDS row (see the header comment).
@@ -176,9 +177,27 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int64_t total = n_blocks * g.n_tiles;
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   const int64_t pid = blockIdx.x;
-  const int64_t local = pid / kXcds;
-  if (local >= per_xcd) return;
-  const int64_t t = (pid % kXcds) * per_xcd + local;
+  int64_t t;
+  if (g.tile_order == 0) {
+    const int64_t local = pid / kXcds;
+    if (local >= per_xcd) return;
+    t = (pid % kXcds) * per_xcd + local;
+  } else if (g.tile_order == 1) {
+    // Shuffled arrival order: bit reversal within the next power of two,
+    // walked back into [0, total) (bit reversal is an involution, so a
+    // reversed index outside the range maps the id to itself: a bijection).
+    if (pid >= total) return;
+    int m = 0;
+    while (((int64_t)1 << m) < total) ++m;
+    const int64_t r = m ? (int64_t)(__builtin_bitreverse64((uint64_t)pid) >> (64 - m)) : 0;
+    t = r < total ? r : pid;
+  } else {
+    // Half-phase: the first and second halves of the expert-major order,
+    // interleaved tile by tile.
+    if (pid >= total) return;
+    const int64_t half = (total + 1) / 2;
+    t = (pid & 1) ? half + pid / 2 : pid / 2;
+  }
   if (t >= total) return;
   const int64_t bq = t / g.n_tiles;  // a block of the tile's run
   const int e = g.eids[bq];
@@ -572,17 +591,19 @@ static bool offsets_fit(int64_t rows, int64_t N, int64_t K) {
 
 using namespace moe;
 
-extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void* B,
-                                const float* B_scale, const int32_t* sorted_ids,
-                                const int32_t* expert_ids, const int32_t* ntpp,
-                                const float* topk_weights, int64_t S, int32_t top_k,
-                                int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
-                                int64_t max_padded, void* C, void* stream) {
+extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
+                                        const float* B_scale, const int32_t* sorted_ids,
+                                        const int32_t* expert_ids, const int32_t* ntpp,
+                                        const float* topk_weights, int64_t S, int32_t top_k,
+                                        int32_t a_by_pos, int64_t N, int64_t K, int32_t E,
+                                        int32_t BM, int64_t max_padded, int32_t tile_order,
+                                        void* C, void* stream) {
   if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
   if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
   if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (tile_order < 0 || tile_order > 2) return kErrBadShape;
   if (max_padded == 0 || S == 0) return kOk;
   if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
     return kErrNullPointer;
@@ -608,7 +629,19 @@ extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void*
   g.top_k = top_k;
   g.a_by_pos = a_by_pos ? 1 : 0;
   g.E = E;
+  g.tile_order = tile_order;
   return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void* B,
+                                const float* B_scale, const int32_t* sorted_ids,
+                                const int32_t* expert_ids, const int32_t* ntpp,
+                                const float* topk_weights, int64_t S, int32_t top_k,
+                                int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
+                                int64_t max_padded, void* C, void* stream) {
+  return moe_grouped_gemm_ordered(A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp,
+                                  topk_weights, S, top_k, a_by_pos, N, K, E, BM, max_padded, 0, C,
+                                  stream);
 }
 
 extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,

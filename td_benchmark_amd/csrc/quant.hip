@@ -1,4 +1,5 @@
-// A1 / A7: dynamic 1x128 per-token-group FP8 quant of bf16 activations.
+// A1 / A7: dynamic 1x128 per-token-group FP8 quant of bf16 activations, and
+//          the standalone SiLU*up + 1x128 quant (A6 + A7) of the unfused chain.
 // A2:      128x128 block FP8 quant of fp32 weights (build time).
 //
 // Arithmetic follows reference moe_bench/verify.py:108-117 and
@@ -18,30 +19,52 @@ constexpr int kQuantThreads = 256;
 constexpr int kQuantUnroll = 4;  // chunks (16 B) per thread
 constexpr int kQuantChunksPerBlock = kQuantThreads * kQuantUnroll;
 
+// SWIGLU = false: x [rows, W] bf16 is quantised directly (A1 / A7).
+// SWIGLU = true:  x [rows, 2W] bf16 holds gate | up; the quantised value is
+//   h = bf16(silu(gate) * up) (A6 then A7, the standalone form of what the
+//   fused W13 epilogue does), with the same rounding chain as the separate
+//   silu_and_mul and quant kernels, so the codes agree bit for bit.
+// A chunk is 8 consecutive output columns of one row; W/8 chunks per row.
+template <bool SWIGLU>
 __global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ s,
-    int64_t n_chunks) {
+    int64_t n_chunks, int64_t chunks_per_row) {
   const int tid = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * kQuantChunksPerBlock;
-  v4i raw[kQuantUnroll];
+  constexpr int NLOAD = SWIGLU ? 2 : 1;
+  v4i raw[kQuantUnroll][NLOAD];
 #pragma unroll
   for (int i = 0; i < kQuantUnroll; ++i) {
-    int64_t ch = base + tid + i * kQuantThreads;
+    const int64_t ch = base + tid + i * kQuantThreads;
     if (ch < n_chunks) {
-      raw[i] = *reinterpret_cast<const v4i*>(x + ch * 8);
+      if constexpr (SWIGLU) {
+        const int64_t r = ch / chunks_per_row, cc = ch % chunks_per_row;
+        const uint16_t* row = x + r * chunks_per_row * 16;
+        raw[i][0] = *reinterpret_cast<const v4i*>(row + cc * 8);
+        raw[i][NLOAD - 1] = *reinterpret_cast<const v4i*>(row + chunks_per_row * 8 + cc * 8);
+      } else {
+        raw[i][0] = *reinterpret_cast<const v4i*>(x + ch * 8);
+      }
     } else {
-      raw[i] = (v4i){0, 0, 0, 0};
+#pragma unroll
+      for (int l = 0; l < NLOAD; ++l) raw[i][l] = (v4i){0, 0, 0, 0};
     }
   }
 #pragma unroll
   for (int i = 0; i < kQuantUnroll; ++i) {
-    int64_t ch = base + tid + i * kQuantThreads;
+    const int64_t ch = base + tid + i * kQuantThreads;
     float v[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t w = (uint32_t)raw[i][j];
-      v[2 * j] = __uint_as_float(w << 16);
-      v[2 * j + 1] = __uint_as_float(w & 0xFFFF0000u);
+      const uint32_t w = (uint32_t)raw[i][0][j];
+      if constexpr (SWIGLU) {
+        const uint32_t u = (uint32_t)raw[i][NLOAD - 1][j];
+        v[2 * j] = silu_mul_bf16(lo_bf16(w), lo_bf16(u));
+        v[2 * j + 1] = silu_mul_bf16(hi_bf16(w), hi_bf16(u));
+      } else {
+        v[2 * j] = lo_bf16(w);
+        v[2 * j + 1] = hi_bf16(w);
+      }
     }
     float amax = 0.0f;
 #pragma unroll
@@ -51,12 +74,12 @@ __global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     amax = fmaxf(amax, __shfl_xor(amax, 4));
     amax = fmaxf(amax, __shfl_xor(amax, 8));
-    float sc = group_scale(amax);
-    float inv = 1.0f / sc;
-    uint32_t lo = pack4_e4m3(clamp_fp8(div_by(v[0], sc, inv)), clamp_fp8(div_by(v[1], sc, inv)),
-                             clamp_fp8(div_by(v[2], sc, inv)), clamp_fp8(div_by(v[3], sc, inv)));
-    uint32_t hi = pack4_e4m3(clamp_fp8(div_by(v[4], sc, inv)), clamp_fp8(div_by(v[5], sc, inv)),
-                             clamp_fp8(div_by(v[6], sc, inv)), clamp_fp8(div_by(v[7], sc, inv)));
+    const float sc = group_scale(amax);
+    const float inv = 1.0f / sc;
+    const uint32_t lo = pack4_e4m3(clamp_fp8(div_by(v[0], sc, inv)), clamp_fp8(div_by(v[1], sc, inv)),
+                                   clamp_fp8(div_by(v[2], sc, inv)), clamp_fp8(div_by(v[3], sc, inv)));
+    const uint32_t hi = pack4_e4m3(clamp_fp8(div_by(v[4], sc, inv)), clamp_fp8(div_by(v[5], sc, inv)),
+                                   clamp_fp8(div_by(v[6], sc, inv)), clamp_fp8(div_by(v[7], sc, inv)));
     if (ch < n_chunks) {
       *reinterpret_cast<uint2*>(q + ch * 8) = make_uint2(lo, hi);
       if ((tid & 15) == 0) s[ch >> 4] = sc;
@@ -127,9 +150,24 @@ extern "C" int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void
   if (((uintptr_t)x_bf16 & 15) != 0 || ((uintptr_t)q_fp8 & 7) != 0) return kErrBadShape;
   const int64_t n_chunks = T * H / 8;
   const int64_t blocks = (n_chunks + kQuantChunksPerBlock - 1) / kQuantChunksPerBlock;
-  hipLaunchKernelGGL(quant_group128_kernel, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
+  hipLaunchKernelGGL(quant_group128_kernel<false>, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x_bf16, (uint8_t*)q_fp8, scales,
-                     n_chunks);
+                     n_chunks, H / 8);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_silu_mul_quant_group128(const void* c_bf16, int64_t R, int64_t I, void* q_fp8,
+                                           float* scales, void* stream) {
+  if (R < 0 || I < 0) return kErrBadShape;
+  if (R == 0 || I == 0) return kOk;
+  if (!c_bf16 || !q_fp8 || !scales) return kErrNullPointer;
+  if (I % 128 != 0) return kErrBadShape;
+  if (((uintptr_t)c_bf16 & 15) != 0 || ((uintptr_t)q_fp8 & 7) != 0) return kErrBadShape;
+  const int64_t n_chunks = R * I / 8;
+  const int64_t blocks = (n_chunks + kQuantChunksPerBlock - 1) / kQuantChunksPerBlock;
+  hipLaunchKernelGGL(quant_group128_kernel<true>, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)c_bf16, (uint8_t*)q_fp8, scales,
+                     n_chunks, I / 8);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -19,6 +19,8 @@ from ._lib import check, lib
 FP8 = torch.float8_e4m3fn
 BLOCK_SHAPE = [128, 128]
 SUPPORTED_BLOCK_M = (16, 32, 64, 128)
+# workgroup -> tile orders of the grouped GEMM (include/moe_mi355x.h)
+TILE_ORDERS = {"expert_major": 0, "shuffled": 1, "half_phase": 2}
 
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
@@ -148,10 +150,12 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                               use_int8_w8a8: bool = False, use_int8_w8a16: bool = False,
                               use_int4_w4a16: bool = False, per_channel_quant: bool = False,
                               block_shape: list[int] | None = None, B_bias: Any = None,
-                              a_by_pos: bool = False) -> None:
+                              a_by_pos: bool = False, tile_order: int = 0) -> None:
     """The reference's grouped-GEMM call (overlap/kernels.py:288-310,
     schemes/shared_expert.py:102-123) on the FP8 w8a8 block-[128,128] form.
-    C is [M, top_k, N] or [S, 1, N]; rows are written by slot."""
+    C is [M, top_k, N] or [S, 1, N]; rows are written by slot.  ``tile_order``
+    selects the workgroup -> tile order (TILE_ORDERS); results do not depend
+    on it."""
     if not use_fp8_w8a8 or use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or per_channel_quant:
         raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
     if B_zp is not None or B_bias is not None:
@@ -169,10 +173,11 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         if topk_weights is None:
             raise ValueError("mul_routed_weight requires topk_weights")
         w = topk_weights.contiguous().view(-1)
-    check(lib().moe_grouped_gemm(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids),
-                                 _ptr(expert_ids), _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
-                                 1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(), _ptr(C),
-                                 _stream()), "moe_grouped_gemm")
+    check(lib().moe_grouped_gemm_ordered(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale),
+                                         _ptr(sorted_token_ids), _ptr(expert_ids),
+                                         _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
+                                         1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(),
+                                         int(tile_order), _ptr(C), _stream()), "moe_grouped_gemm")
 
 
 def _block_m_from(sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor) -> int:
@@ -219,13 +224,39 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
     check(lib().moe_silu_and_mul(_ptr(x), R, I, _ptr(out), _stream()), "moe_silu_and_mul")
 
 
-def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int) -> torch.Tensor:
+def silu_mul_quant_group128(x: torch.Tensor, out_q: torch.Tensor | None = None,
+                            out_s: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [R, 2I] bf16 (gate | up) -> FP8 1x128 quant of bf16(silu(gate)*up):
+    (q [R, I] e4m3fn, scales [R, I/128]).  One pass of silu_and_mul followed by
+    moe_kernel_quantize_input (overlap/overlap_forward.py:277-284)."""
+    _need(x, "x", torch.bfloat16)
+    R = x.numel() // x.shape[-1]
+    I = x.shape[-1] // 2
+    q = torch.empty((R, I), dtype=FP8, device=x.device) if out_q is None else out_q
+    s = torch.empty((R, I // 128), dtype=torch.float32, device=x.device) if out_s is None else out_s
+    check(lib().moe_silu_mul_quant_group128(_ptr(x), R, I, _ptr(q), _ptr(s), _stream()),
+          "moe_silu_mul_quant_group128")
+    return q, s
+
+
+def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int,
+            addend: torch.Tensor | None = None) -> torch.Tensor:
     """out[t] = sum_i D[t*k+i] (fp32 accumulation, bf16 result), the reference's
-    torch.sum(C_down.view(T,k,H), dim=1) (overlap/overlap_forward.py:304-313)."""
+    torch.sum(C_down.view(T,k,H), dim=1) (overlap/overlap_forward.py:304-313).
+    With ``addend`` ([T, H] bf16, the shared expert's output) the bf16 sum is
+    added to it in the same pass, as ``result + shared(hidden)`` does
+    (schemes/vllm_tp.py:62-63)."""
     _need(D, "D", torch.bfloat16)
     _need(out, "out", torch.bfloat16)
     T, H = out.shape
-    check(lib().moe_reduce_topk(_ptr(D), T, top_k, H, _ptr(out), _stream()), "moe_reduce_topk")
+    if addend is None:
+        check(lib().moe_reduce_topk(_ptr(D), T, top_k, H, _ptr(out), _stream()), "moe_reduce_topk")
+    else:
+        _need(addend, "addend", torch.bfloat16)
+        if tuple(addend.shape) != (T, H):
+            raise ValueError(f"addend must be [{T}, {H}]")
+        check(lib().moe_reduce_topk_add(_ptr(D), _ptr(addend), T, top_k, H, _ptr(out), _stream()),
+              "moe_reduce_topk_add")
     return out
 
 
@@ -253,15 +284,85 @@ def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, i
 # A10 -- the whole layer
 # ---------------------------------------------------------------------------
 
+class SharedExpertRunner:
+    """The shared expert (E = 1, top-1) through the same kernels, with every
+    buffer and the align outputs built once (schemes/shared_expert.py:15-148).
+
+    ``__call__(x, input_scale=None)``: a bf16 ``x`` [rows, H] is quantised
+    1x128 first; an FP8 ``x`` is used directly with its [rows, H/128]
+    ``input_scale`` -- no dequantise/requantise round trip
+    (shared_expert.py:3-7, 83-93).  Returns a [rows, H] bf16 view of an
+    internal buffer (valid until the next call)."""
+
+    def __init__(self, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
+                 w2_scale: torch.Tensor, max_tokens: int, block_size_m: int | None = None):
+        for name, t in (("w1", w1), ("w2", w2)):
+            _need(t, name, FP8)
+        if w1.shape[0] != 1 or w2.shape[0] != 1:
+            raise ValueError("the shared expert has exactly one expert")
+        _, N2, H = w1.shape
+        if w2.shape != (1, H, N2 // 2):
+            raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w1 {tuple(w1.shape)}")
+        self.w1, self.w1_scale, self.w2, self.w2_scale = w1, w1_scale, w2, w2_scale
+        self.H, self.I, self.max_tokens = H, N2 // 2, max_tokens
+        self.BM = block_size_m or get_moe_config(max_tokens, 1, 1)["BLOCK_SIZE_M"]
+        dev = w1.device
+        self._aligns: dict[int, AlignBuffers] = {}
+        self._align_for(max_tokens)
+        mp = self._aligns[max_tokens].max_padded
+        self.q = torch.empty((max_tokens, H), dtype=FP8, device=dev)
+        self.s = torch.empty((max_tokens, H // 128), dtype=torch.float32, device=dev)
+        self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
+        self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
+        self.out = torch.empty((max_tokens, H), dtype=torch.bfloat16, device=dev)
+
+    def _align_for(self, rows: int) -> AlignBuffers:
+        """Align outputs for `rows` tokens routed to expert 0 (built once per row count)."""
+        a = self._aligns.get(rows)
+        if a is None:
+            a = AlignBuffers(rows, 1, self.BM, self.w1.device)
+            a.run(torch.zeros(rows, dtype=torch.int32, device=self.w1.device))
+            self._aligns[rows] = a
+        return a
+
+    def __call__(self, x: torch.Tensor, input_scale: torch.Tensor | None = None) -> torch.Tensor:
+        rows = x.shape[0]
+        if rows > self.max_tokens:
+            raise ValueError(f"{rows} rows exceed max_tokens={self.max_tokens}")
+        if x.dtype == FP8:
+            if input_scale is None:
+                raise ValueError("FP8 shared expert input requires input_scale")
+            if input_scale.shape[0] != rows:
+                raise ValueError(f"input_scale rows {input_scale.shape[0]} do not match input rows {rows}")
+            q, s = x, input_scale
+        else:
+            q, s = per_token_group_quant_fp8(x, out_q=self.q[:rows], out_s=self.s[:rows])
+        _need(q, "x", FP8)
+        _need(s, "input_scale", torch.float32)
+        a = self._align_for(rows)
+        check(lib().moe_gemm_w13_silu_quant(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
+                                            _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
+                                            self.H, self.I, 1, self.BM, a.max_padded, _ptr(self.hq),
+                                            _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
+        out = self.out[:rows]
+        check(lib().moe_grouped_gemm(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
+                                     _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), None, rows, 1, 1,
+                                     self.H, self.I, 1, self.BM, a.max_padded, _ptr(out), _stream()),
+              "moe_grouped_gemm")
+        return out
+
+
 class FusedExpertsRunner:
     """Prebuilt A1->A9 chain for fixed (T, H, I, E, top_k, BM).
 
     Construction allocates every buffer; ``run`` only enqueues kernels
-    (quant -> align -> W13+SiLU+quant -> W2 with routed weights -> top-k sum)
-    on the current stream and returns the [T, H] bf16 output buffer."""
+    (quant -> align -> W13+SiLU+quant -> W2 with routed weights ->
+    [shared expert on the same FP8 input] -> top-k sum) on the current stream
+    and returns the [T, H] bf16 output (``out`` if one was given)."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
-                 w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None):
+                 w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
+                 shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None):
         for name, t in (("w13", w13), ("w2", w2)):
             _need(t, name, FP8)
         _need(w13_scale, "w13_scale", torch.float32)
@@ -274,7 +375,11 @@ class FusedExpertsRunner:
         self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
         if self.BM not in SUPPORTED_BLOCK_M:
             raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
+        if shared is not None and (shared.H != H or shared.max_tokens < num_tokens):
+            raise ValueError("shared expert does not match the layer's hidden size / token count")
         self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
+        self.shared = shared
+        self.shared_out: torch.Tensor | None = None
         dev = w13.device
         self.q1 = torch.empty((self.T, H), dtype=FP8, device=dev)
         self.s1 = torch.empty((self.T, H // 128), dtype=torch.float32, device=dev)
@@ -283,7 +388,11 @@ class FusedExpertsRunner:
         self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
         self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
         self.D = torch.empty((max(self.S, 1), H), dtype=torch.bfloat16, device=dev)
-        self.y = torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
+        if out is not None:
+            _need(out, "out", torch.bfloat16)
+            if tuple(out.shape) != (self.T, H):
+                raise ValueError(f"out must be [{self.T}, {H}]")
+        self.y = out if out is not None else torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
 
     def stage_quant(self, hidden: torch.Tensor) -> None:
         _need(hidden, "hidden_states", torch.bfloat16)
@@ -311,16 +420,67 @@ class FusedExpertsRunner:
                                      _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
                                      a.max_padded, _ptr(self.D), _stream()), "moe_grouped_gemm")
 
+    def stage_shared(self) -> None:
+        """The shared expert on the layer's own FP8 input (no second quant)."""
+        if self.shared is not None:
+            self.shared_out = self.shared(self.q1, self.s1)
+
     def stage_reduce(self) -> None:
-        check(lib().moe_reduce_topk(_ptr(self.D), self.T, self.top_k, self.H, _ptr(self.y), _stream()),
-              "moe_reduce_topk")
+        moe_sum(self.D[: self.S], self.y, self.top_k,
+                addend=self.shared_out if self.shared is not None else None)
 
     def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
         self.stage_quant(hidden)
         self.stage_align(topk_ids)
         self.stage_w13()
         self.stage_w2(topk_weights)
+        self.stage_shared()
         self.stage_reduce()
+        return self.y
+
+
+class ChunkedExpertsRunner:
+    """The layer over ``n_chunks`` token chunks pipelined on ``n_streams`` HIP
+    streams of one device (the chunked quant/align/GEMM overlap of
+    overlap/overlap_forward.py:252-321, single-GPU form).  Chunk c runs its
+    whole chain on stream c mod n_streams; the streams start after the caller's
+    stream and the caller's stream waits for all of them before ``run``
+    returns (overlap_forward.py:336-342).  Each chunk writes its rows of the
+    shared [T, H] output directly."""
+
+    def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
+                 w2_scale: torch.Tensor, num_tokens: int, top_k: int, n_chunks: int, n_streams: int,
+                 block_size_m: int | None = None, shared_weights: tuple | None = None):
+        if n_chunks < 1 or n_streams < 1:
+            raise ValueError("n_chunks and n_streams must be >= 1")
+        n_chunks = min(n_chunks, num_tokens) if num_tokens > 0 else 1
+        self.T, self.top_k, self.H = num_tokens, top_k, w13.shape[2]
+        self.y = torch.empty((num_tokens, self.H), dtype=torch.bfloat16, device=w13.device)
+        bounds = [num_tokens * c // n_chunks for c in range(n_chunks + 1)]
+        self.bounds = list(zip(bounds[:-1], bounds[1:]))
+        # one shared-expert runner per chunk (weights shared, buffers per chunk)
+        self.runners = [FusedExpertsRunner(w13, w13_scale, w2, w2_scale, r1 - r0, top_k, block_size_m,
+                                           shared=(SharedExpertRunner(*shared_weights, max_tokens=r1 - r0)
+                                                   if shared_weights is not None else None),
+                                           out=self.y[r0:r1]) for r0, r1 in self.bounds]
+        # default-priority streams
+        self.streams = [torch.cuda.Stream(device=w13.device) for _ in range(min(n_streams, n_chunks))]
+
+    def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
+        caller = torch.cuda.current_stream()
+        start = torch.cuda.Event()
+        start.record(caller)
+        for st in self.streams:
+            st.wait_event(start)
+        k = self.top_k
+        w, ids = topk_weights.reshape(-1), topk_ids.reshape(-1)
+        for c, ((r0, r1), runner) in enumerate(zip(self.bounds, self.runners)):
+            with torch.cuda.stream(self.streams[c % len(self.streams)]):
+                runner.run(hidden[r0:r1], w[r0 * k:r1 * k], ids[r0 * k:r1 * k])
+        for st in self.streams:
+            done = torch.cuda.Event()
+            done.record(st)
+            caller.wait_event(done)
         return self.y
 
 
