@@ -18,10 +18,13 @@
 //      giving each slot its rank among equal-expert slots of its wave; per-wave
 //      counts in LDS are prefix-summed across the 16 waves, giving each slot its
 //      rank within the chunk and each chunk its per-expert count.
-//   2. scan:   one workgroup scans the chunk counts per expert (column-wise),
-//      pads, scans across experts, writes expert_ids / ntpp / pad fill, and
-//      turns the chunk counts into chunk base positions.
-//   3. place:  sorted_ids[chunk_base[chunk][e] + rank[s]] = s.
+//   2. scan:   one workgroup scans the chunk counts per expert (column-wise,
+//      from LDS), pads, scans across experts, and writes the expert offsets,
+//      counts and ntpp; the chunk counts become within-expert chunk bases.
+//   3. place:  a wide pass: sorted_ids[off[e] + chunk_base[chunk][e] + rank[s]]
+//      = s for every slot, S at every padding position, and expert_ids for
+//      every block (the expert of a position comes from a binary search over
+//      the offsets held in LDS).
 // Align moves well under 2 MB at every configuration, so it is latency-bound.
 #include "common.hpp"
 
@@ -29,6 +32,7 @@ namespace moe {
 
 constexpr int kAlignChunk = 1024;   // slots per count workgroup (16 waves)
 constexpr int kAlignMaxExperts = 1024;
+constexpr int64_t kAlignStageLimit = 32768;  // chunk counts staged in LDS up to 128 KiB
 
 __global__ __launch_bounds__(kAlignChunk) void align_count_kernel(
     const int32_t* __restrict__ ids, int64_t S, int E, int nbits,
@@ -67,31 +71,47 @@ __global__ __launch_bounds__(kAlignChunk) void align_count_kernel(
   if (valid) rank[s] = wcnt[wave * E + e] + rank_in_wave;
 }
 
+// One workgroup: per-expert totals and the within-expert base of every chunk
+// (column prefix sums of the chunk counts, staged in LDS when they fit), then
+// padded sizes and their exclusive scan across experts.  Writes off[0..E]
+// (off[E] = ntpp), cnt[0..E) and ntpp; every fill is left to the wide place
+// kernel.
 __global__ __launch_bounds__(kAlignMaxExperts) void align_scan_kernel(
-    int32_t* __restrict__ chunk_count, int64_t n_chunks, int E, int BM, int64_t S,
-    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ ntpp_out, int64_t max_padded) {
-  __shared__ int32_t pad_scan[kAlignMaxExperts];
+    int32_t* __restrict__ chunk_count, int64_t n_chunks, int E, int BM, int use_lds,
+    int32_t* __restrict__ off_out, int32_t* __restrict__ cnt_out, int32_t* __restrict__ ntpp_out) {
+  extern __shared__ int32_t staged[];  // [n_chunks][E] when use_lds
   __shared__ int32_t wave_tot[kAlignMaxExperts / 64];
   const int tid = threadIdx.x;
   const int e = tid;
+  if (use_lds) {
+    for (int64_t i = tid; i < n_chunks * E; i += kAlignMaxExperts) staged[i] = chunk_count[i];
+    __syncthreads();
+  }
   int cnt = 0;
   if (e < E) {
-    int64_t c = 0;
-    for (; c + 8 <= n_chunks; c += 8) {
-      int v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = chunk_count[(c + j) * E + e];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        chunk_count[(c + j) * E + e] = cnt;
-        cnt += v[j];
+    if (use_lds) {
+      for (int64_t c = 0; c < n_chunks; ++c) {
+        const int v = staged[c * E + e];
+        chunk_count[c * E + e] = cnt;
+        cnt += v;
       }
-    }
-    for (; c < n_chunks; ++c) {
-      int v = chunk_count[c * E + e];
-      chunk_count[c * E + e] = cnt;
-      cnt += v;
+    } else {
+      int64_t c = 0;
+      for (; c + 8 <= n_chunks; c += 8) {
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = chunk_count[(c + j) * E + e];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          chunk_count[(c + j) * E + e] = cnt;
+          cnt += v[j];
+        }
+      }
+      for (; c < n_chunks; ++c) {
+        const int v = chunk_count[c * E + e];
+        chunk_count[c * E + e] = cnt;
+        cnt += v;
+      }
     }
   }
   const int padded = (e < E) ? (cnt + BM - 1) / BM * BM : 0;
@@ -100,43 +120,72 @@ __global__ __launch_bounds__(kAlignMaxExperts) void align_scan_kernel(
   int incl = padded;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(incl, o);
+    const int y = __shfl_up(incl, o);
     if (lane >= o) incl += y;
   }
   if (lane == 63) wave_tot[wave] = incl;
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kAlignMaxExperts / 64; ++w) {
-      int t = wave_tot[w];
-      wave_tot[w] = run;
-      run += t;
+  if (tid < 64) {
+    // exclusive scan of the 16 wave totals by the first wave
+    const int t = tid < kAlignMaxExperts / 64 ? wave_tot[tid] : 0;
+    int x = t;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
     }
-    pad_scan[0] = run;  // total, read below after the barrier
+    if (tid < kAlignMaxExperts / 64) wave_tot[tid] = x - t;
+    if (tid == kAlignMaxExperts / 64 - 1) {
+      off_out[E] = x;
+      *ntpp_out = x;
+    }
   }
   __syncthreads();
-  const int total = pad_scan[0];
-  const int off = wave_tot[wave] + incl - padded;
   if (e < E) {
-    for (int64_t c = 0; c < n_chunks; ++c) chunk_count[c * E + e] += off;
-    for (int b = off / BM; b < (off + padded) / BM; ++b) expert_ids[b] = e;
-    for (int p = off + cnt; p < off + padded; ++p) sorted_ids[p] = (int32_t)S;
+    off_out[e] = wave_tot[wave] + incl - padded;
+    cnt_out[e] = cnt;
   }
-  const int64_t max_blocks = (max_padded + BM - 1) / BM;
-  for (int64_t b = total / BM + tid; b < max_blocks; b += kAlignMaxExperts) expert_ids[b] = -1;
-  for (int64_t p = total + tid; p < max_padded; p += kAlignMaxExperts) sorted_ids[p] = (int32_t)S;
-  if (tid == 0) *ntpp_out = total;
 }
 
+// Wide pass over max(S, max_padded) indices: slot i goes to
+// off[e] + chunk_base[chunk][e] + rank[i]; position i is set to S when it is
+// padding (inside an expert's run past its count, or past ntpp), and the first
+// position of every block writes that block's expert (-1 past ntpp).  Valid
+// and padding positions are disjoint, so no two threads write one element.
 __global__ __launch_bounds__(256) void align_place_kernel(
-    const int32_t* __restrict__ ids, int64_t S, int E, const int32_t* __restrict__ chunk_base,
-    const int32_t* __restrict__ rank, int32_t* __restrict__ sorted_ids) {
-  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (s >= S) return;
-  const int e = ids[s];
-  if (e < 0 || e >= E) return;
-  const int64_t chunk = s / kAlignChunk;
-  sorted_ids[chunk_base[chunk * E + e] + rank[s]] = (int32_t)s;
+    const int32_t* __restrict__ ids, int64_t S, int E, int BM, const int32_t* __restrict__ chunk_base,
+    const int32_t* __restrict__ rank, const int32_t* __restrict__ off, const int32_t* __restrict__ cnt,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids, int64_t max_padded) {
+  __shared__ int32_t s_off[kAlignMaxExperts + 1];
+  __shared__ int32_t s_cnt[kAlignMaxExperts];
+  for (int i = threadIdx.x; i <= E; i += 256) s_off[i] = off[i];
+  for (int i = threadIdx.x; i < E; i += 256) s_cnt[i] = cnt[i];
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < S) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) {
+      const int64_t chunk = i / kAlignChunk;
+      sorted_ids[s_off[e] + chunk_base[chunk * E + e] + rank[i]] = (int32_t)i;
+    }
+  }
+  if (i < max_padded) {
+    const int total = s_off[E];
+    int e = -1;
+    bool pad = true;
+    if (i < total) {
+      int lo = 0, hi = E - 1;  // largest e with off[e] <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_off[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      e = lo;
+      pad = (i - s_off[e]) >= s_cnt[e];
+    }
+    if (pad) sorted_ids[i] = (int32_t)S;
+    if (i % BM == 0) expert_ids[i / BM] = e;
+  }
 }
 
 }  // namespace moe
@@ -153,7 +202,8 @@ extern "C" int64_t moe_align_max_padded(int64_t S, int32_t E, int32_t BM) {
 extern "C" int64_t moe_align_workspace_bytes(int64_t S, int32_t E) {
   if (S < 0 || E <= 0) return -1;
   const int64_t n_chunks = (S + kAlignChunk - 1) / kAlignChunk;
-  return 4 * (n_chunks * E + S) + 256;
+  // chunk counts [n_chunks][E], rank [S], off [E+1], cnt [E]
+  return 4 * (n_chunks * E + S + 2 * (int64_t)E + 1) + 256;
 }
 
 extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
@@ -170,6 +220,8 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t 
   const int64_t n_chunks = (S + kAlignChunk - 1) / kAlignChunk;
   int32_t* chunk_count = (int32_t*)workspace;
   int32_t* rank = chunk_count + n_chunks * E;
+  int32_t* off = rank + S;
+  int32_t* cnt = off + E + 1;
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   if (n_chunks > 0) {
@@ -177,11 +229,23 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t 
                        16 * E * sizeof(int32_t), st, topk_ids, S, (int)E, nbits, chunk_count,
                        rank);
   }
-  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignMaxExperts), 0, st, chunk_count,
-                     n_chunks, (int)E, (int)BM, S, sorted_ids, expert_ids, ntpp, max_padded);
-  if (S > 0) {
-    hipLaunchKernelGGL(align_place_kernel, dim3((unsigned)((S + 255) / 256)), dim3(256), 0, st,
-                       topk_ids, S, (int)E, chunk_count, rank, sorted_ids);
+  // Stage the chunk counts in LDS when they fit (128 KiB of the 160 KiB).
+  static bool lds_attr = false;
+  if (!lds_attr) {
+    if (hipFuncSetAttribute((const void*)align_scan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(kAlignStageLimit * sizeof(int32_t))) != hipSuccess)
+      return kErrLaunch;
+    lds_attr = true;
+  }
+  const int use_lds = n_chunks * E <= kAlignStageLimit ? 1 : 0;
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignMaxExperts),
+                     use_lds ? (size_t)(n_chunks * E * sizeof(int32_t)) : 0, st, chunk_count, n_chunks,
+                     (int)E, (int)BM, use_lds, off, cnt, ntpp);
+  const int64_t wide = S > max_padded ? S : max_padded;
+  if (wide > 0) {
+    hipLaunchKernelGGL(align_place_kernel, dim3((unsigned)((wide + 255) / 256)), dim3(256), 0, st,
+                       topk_ids, S, (int)E, (int)BM, chunk_count, rank, off, cnt, sorted_ids,
+                       expert_ids, max_padded);
   }
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

@@ -18,6 +18,7 @@ namespace moe {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 constexpr float kFp8Max = 448.0f;
 constexpr float kScaleFloor = 1e-12f;   // verify.py:115 clamp(min=1e-12)

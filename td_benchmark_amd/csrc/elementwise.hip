@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __rest
   v4i rows[KMAX];
 #pragma unroll
   for (int i = 0; i < KMAX; ++i)
-    if (i < k) rows[i] = *reinterpret_cast<const v4i*>(D + (t * k + i) * H + cc * 8);
+    if (i < k) rows[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(D + (t * k + i) * H + cc * 8));
   v4i add = {0, 0, 0, 0};
   if constexpr (ADD) add = *reinterpret_cast<const v4i*>(addend + t * H + cc * 8);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __rest
     }
     out[j] = (int)(lo | (hi << 16));
   }
-  *reinterpret_cast<v4i*>(y + t * H + cc * 8) = out;
+  __builtin_nontemporal_store(out, reinterpret_cast<v4i*>(y + t * H + cc * 8));
 }
 
 __global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __restrict__ c,

@@ -168,8 +168,9 @@ void grouped_gemm_kernel(GemmArgs g) {
   // ---- expert-aligned, XCD-aware tile mapping ----------------------------
   // Tiles are ordered run-major: for each run of consecutive blocks with the
   // same expert (blocks [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT),
-  // n-tile major and block minor, so the n blocks that read one weight tile
-  // are adjacent.  Workgroup ids are dealt round-robin to the XCDs; XCD x
+  // in groups of a few n-tiles (all n blocks of the run inside a group), so
+  // the blocks that read one weight tile are close together.  Workgroup ids
+  // are dealt round-robin to the XCDs; XCD x
   // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
   // the same time on one XCD and fetch the weight tile from HBM once.
   const int ntpp = *g.ntpp;
@@ -225,9 +226,16 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
   const int64_t b0 = bq - back;
   const int64_t run = back + 1 + fwd;
+  // Inside a run, n-tiles go in groups of GG, block-major within a group:
+  // the GG workgroups that share an A block start together and reuse it from
+  // L2, and a weight tile is still read by all blocks of the run close in time.
   const int64_t in_run = t - b0 * g.n_tiles;
-  const int64_t j = in_run / run;
-  const int64_t b = b0 + in_run % run;
+  constexpr int64_t GG = FUSED ? 4 : 2;
+  const int64_t gj0 = in_run / (GG * run) * GG;
+  const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
+  const int64_t in_grp = in_run - gj0 * run;
+  const int64_t b = b0 + in_grp / gsz;
+  const int64_t j = gj0 + in_grp % gsz;
   const int64_t K = g.K;
   const int KB = (int)(K / 128);
   const int64_t NBt = g.N / 128;

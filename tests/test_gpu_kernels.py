@@ -153,6 +153,7 @@ ALIGN_CASES = [
     (8192, 8, 256, 128, "sigmoid"),   # DSv3 size, S = 65536
     (4096, 8, 128, 64, "softmax"),    # multiple chunks, E=128
     (1000, 3, 1000, 32, "softmax"),   # E close to the 1024 limit
+    (16384, 8, 512, 128, "softmax"),  # chunk counts too large to stage in LDS
 ]
 
 
