@@ -17,8 +17,10 @@
 // 282-284), writing FP8 codes + scales by sorted position so that the W2 GEMM
 // reads its A rows contiguously.
 //
-// Tiling: one workgroup = 4 waves = 256 threads computes BM rows (one expert
-// block) x 256 B-rows (two 128-row scale groups); the K step is 128 = one
+// Tiling: one workgroup computes BM rows (one expert block) x 256 B-rows (two
+// 128-row scale groups) with 8 waves (2 per SIMD, so one wave's MFMAs run
+// while the other waits on LDS or the barrier) for BM >= 32, and with 4 waves
+// for BM = 16 (too few rows to split).  The K step is 128 = one
 // scale block, and every K step is exactly one 16x16x128 MFMA per 16x16
 // output subtile started from zero, so the per-block scales are applied as
 // acc = fma(partial, a_s[row]*b_s[group], acc) with no second accumulator.
@@ -59,15 +61,16 @@
 
 namespace moe {
 
-constexpr int kGemmThreads = 256;
 constexpr int kXcds = 8;
 constexpr int kStages = 3;
 constexpr int kMaxKB = 128;  // K <= 16384
 
 template <int BM>
 struct Tile {
-  static constexpr int WM = (BM == 128) ? 2 : 1;  // waves along M
-  static constexpr int WN = 4 / WM;               // waves along N
+  static constexpr int NW = BM >= 32 ? 8 : 4;     // waves per workgroup (2 per SIMD at 8)
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WM = (NW == 8 || BM == 128) ? 2 : 1;  // waves along M
+  static constexpr int WN = NW / WM;              // waves along N
   static constexpr int RS = BM / WM / 16;         // 16-row subtiles per wave
   static constexpr int CS = 8 / WN;               // 16-col subtiles per wave per group
   static constexpr int A_BYTES = BM * 128;
@@ -76,13 +79,18 @@ struct Tile {
   static constexpr int NA = BM / 8;               // 1 KiB A DMA instructions per stage
   static constexpr int NB = 32;                   // 1 KiB B DMA instructions per stage
   static constexpr int NS = (BM + 63) / 64;       // 256 B A-scale DMA instructions per stage
-  static constexpr int NA_W = (NA + 3) / 4;       // A instructions of the busiest wave
-  static constexpr int na(int w) { return w < NA ? (NA - w + 3) / 4 : 0; }
-  static constexpr int ns(int w) { return (3 - w) < NS ? 1 : 0; }  // waves 3, 2 issue scales
-  static constexpr int cnt(int w) { return na(w) + NB / 4 + ns(w); }
-  static constexpr int min2(int a, int b) { return a < b ? a : b; }
+  static constexpr int NA_W = (NA + NW - 1) / NW; // A instructions of the busiest wave
+  static constexpr int NB_W = NB / NW;            // B instructions per wave
+  static constexpr int na(int w) { return w < NA ? (NA - w + NW - 1) / NW : 0; }
+  static constexpr int ns(int w) { return (NW - 1 - w) < NS ? 1 : 0; }  // the last waves issue scales
+  static constexpr int cnt(int w) { return na(w) + NB_W + ns(w); }
+  static constexpr int vm_min() {
+    int m = cnt(0);
+    for (int w = 1; w < NW; ++w) m = cnt(w) < m ? cnt(w) : m;
+    return m;
+  }
   // loads of one stage per wave that may stay in flight while the older stage is consumed
-  static constexpr int VM = min2(min2(cnt(0), cnt(1)), min2(cnt(2), cnt(3)));
+  static constexpr int VM = vm_min();
   static constexpr int OFF_SA = kStages * STAGE;
   static constexpr int OFF_SB = OFF_SA + kStages * NS * 256;
   static constexpr int OFF_RED = OFF_SB + 2 * kMaxKB * 4;
@@ -150,7 +158,8 @@ MOE_DEVICE void dma4(const uint8_t* g, uint8_t* lds) {
 }
 
 template <int BM, bool FUSED>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(Tile<BM>::THREADS)
+__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4, Tile<BM>::NW / 4)))
 void grouped_gemm_kernel(GemmArgs g) {
   using T = Tile<BM>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -256,14 +265,14 @@ void grouped_gemm_kernel(GemmArgs g) {
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
     if (FUSED) {
-      for (int ci = tid; ci < BM * 8; ci += kGemmThreads) {
+      for (int ci = tid; ci < BM * 8; ci += T::THREADS) {
         const int row = ci >> 3, cc = ci & 7;
         *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
       }
-      for (int row = tid; row < BM; row += kGemmThreads)
+      for (int row = tid; row < BM; row += T::THREADS)
         g.hs[(b * BM + row) * (g.I / 128) + j] = kScaleFloor;
     } else {
-      for (int ci = tid; ci < BM * 32; ci += kGemmThreads) {
+      for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
         const int row = ci >> 5, cc = ci & 31;
         const int64_t slot = g.sorted[b * BM + row];
         if (slot >= g.S) continue;
@@ -301,7 +310,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   uint32_t a_off[T::NA_W > 0 ? T::NA_W : 1];
 #pragma unroll
   for (int i = 0; i < T::NA_W; ++i) {
-    const int gi = wave + 4 * i;
+    const int gi = wave + T::NW * i;
     const int row = (gi < T::NA) ? 8 * gi + (lane >> 3) : 0;
     const int cc = slot_of(lane & 7, row);
     a_off[i] = (uint32_t)(a_row_of(row) * K) + (uint32_t)(cc * 16);
@@ -317,8 +326,8 @@ void grouped_gemm_kernel(GemmArgs g) {
     const int cc = slot_of(lane & 7, r0);
     b_off = (uint32_t)(r0 * K) + (uint32_t)(cc * 16);
   }
-  // A scales: instruction s (issued by wave 3-s) covers rows 64*s .. 64*s+63.
-  const int s_idx = 3 - wave;
+  // A scales: instruction s (issued by wave NW-1-s) covers rows 64*s .. 64*s+63.
+  const int s_idx = T::NW - 1 - wave;
   uint32_t sa_off = 0;
   if (s_idx < T::NS) {
     const int row = 64 * s_idx + lane;
@@ -332,13 +341,16 @@ void grouped_gemm_kernel(GemmArgs g) {
     const uint8_t* abase = g.A + kk * 128;
 #pragma unroll
     for (int i = 0; i < T::NA_W; ++i) {
-      const int gi = wave + 4 * i;
+      const int gi = wave + T::NW * i;
       if (gi < T::NA) dma16(abase + a_off[i], dst + gi * 1024);
     }
+    // B instruction gi = wave + NW*i covers tile rows 8*gi .. 8*gi+7 (group
+    // i / (NB_W/2), row 8*wave + 8*NW*(i mod NB_W/2) + L/8 inside the group).
+    constexpr int HALF = T::NB_W / 2;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint8_t* bbase = (i < 4 ? b_grp0 : b_grp1) + (int64_t)(32 * (i & 3)) * K + kk * 128;
-      dma16(bbase + b_off, dst + T::A_BYTES + (wave + 4 * i) * 1024);
+    for (int i = 0; i < T::NB_W; ++i) {
+      const uint8_t* bbase = (i < HALF ? b_grp0 : b_grp1) + (int64_t)(8 * T::NW * (i % HALF)) * K + kk * 128;
+      dma16(bbase + b_off, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
     }
     if (s_idx < T::NS)
       dma4(reinterpret_cast<const uint8_t*>(g.As + kk) + sa_off,
@@ -346,7 +358,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   };
 
   // Weight scales of both groups for every K block (read once, plain loads).
-  for (int i = tid; i < 2 * KB; i += kGemmThreads) {
+  for (int i = tid; i < 2 * KB; i += T::THREADS) {
     const int grp = i / KB, kk = i % KB;
     smSB[grp * kMaxKB + kk] = g.Bs[((int64_t)e * NBt + (grp ? g1 : g0)) * KB + kk];
   }
@@ -521,7 +533,7 @@ void grouped_gemm_kernel(GemmArgs g) {
         }
       }
     __syncthreads();
-    for (int ci = tid; ci < BM * 8; ci += kGemmThreads) {
+    for (int ci = tid; ci < BM * 8; ci += T::THREADS) {
       const int row = ci >> 3, cc = ci & 7;
       *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) =
           *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
@@ -545,7 +557,7 @@ void grouped_gemm_kernel(GemmArgs g) {
           }
       }
     __syncthreads();
-    for (int ci = tid; ci < BM * 32; ci += kGemmThreads) {
+    for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
       const int row = ci >> 5, cc = ci & 31;
       const int64_t slot = smSlot[row];
       if (slot >= g.S) continue;
@@ -571,7 +583,7 @@ static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   // Upper bound on the tile count (the real one depends on ntpp, on the device).
   const int64_t grid = (args.max_blocks * args.n_tiles + kXcds - 1) / kXcds * kXcds;
   if (grid <= 0) return kOk;
-  hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(kGemmThreads),
+  hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(T::THREADS),
                      T::LDS_BYTES, st, args);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
