@@ -66,6 +66,16 @@ int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t 
                          int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
                          int64_t max_padded, void* workspace, void* stream);
 
+/* A3 with an expert map (expert parallelism) -- vLLM moe_align_block_size(
+ * topk_ids, BM, E, expert_map) as called at overlap/overlap_forward.py:165-169
+ * and schemes/vllm_ep.py:57-66: the sort and padding run over the E global
+ * experts, then every block's expert id is replaced by expert_map[id] (its
+ * local id, or -1 for an expert on another device; the GEMMs write zeros for
+ * -1 blocks).  expert_map [E] int32. */
+int moe_align_block_size_mapped(const int32_t* topk_ids, int64_t S, int32_t E, int32_t block_size_m,
+                                const int32_t* expert_map, int32_t* sorted_ids, int32_t* expert_ids,
+                                int32_t* ntpp, int64_t max_padded, void* workspace, void* stream);
+
 /* A5 / A8 -- block-scaled FP8 grouped GEMM, plain bf16 epilogue.
  * Replaces vLLM dispatch_fused_moe_kernel(A, B, C, A_scale, B_scale, None,
  * topk_weights, sorted_token_ids, expert_ids, num_tokens_post_padded,
@@ -94,6 +104,36 @@ int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
                              const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
                              int64_t N, int64_t K, int32_t E, int32_t block_size_m,
                              int64_t max_padded, int32_t tile_order, void* C, void* stream);
+
+/* A5 / A8 on an N slice -- the reference's N-split wrapper
+ * invoke_moe_kernel_n_split (overlap/kernels.py:219-310): computes
+ * C[:, N_offset:N_offset+N_chunk] from B[:, N_offset:N_offset+N_chunk, :] and
+ * the matching B_scale groups.  B [E, full_N, K], B_scale [E, full_N/128,
+ * K/128], C [S, full_N] bf16 (other columns untouched).  N_offset, N_chunk,
+ * full_N, K multiples of 128. */
+int moe_grouped_gemm_n_split(const void* A, const float* A_scale, const void* B,
+                             const float* B_scale, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* ntpp,
+                             const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
+                             int64_t full_N, int64_t N_offset, int64_t N_chunk, int64_t K,
+                             int32_t E, int32_t block_size_m, int64_t max_padded, void* C,
+                             void* stream);
+
+/* A5 / A8 over a K window with chunk accumulation -- the reference's K-split
+ * wrapper invoke_moe_kernel_k_split + fused_moe_kernel_accumulate
+ * (overlap/kernels.py:36-214, 317-452): the partial product over
+ * A[:, A_K_offset:+K_chunk] (A [rows, A_cols], scales [rows, A_cols/128]) and
+ * B[:, :, K_offset:+K_chunk] (B [E, N, full_K], scales [E, N/128, full_K/128])
+ * is rounded to bf16 (routed weight applied first) and either stored
+ * (is_first_chunk != 0) or added to C: C = bf16(C + partial).  Expert -1 blocks
+ * write zeros on the first chunk only.  C [S, N] bf16. */
+int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int64_t A_cols, int64_t A_K_offset,
+                             const void* B, const float* B_scale, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* ntpp,
+                             const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
+                             int64_t N, int64_t full_K, int64_t K_offset, int64_t K_chunk, int32_t E,
+                             int32_t block_size_m, int64_t max_padded, int32_t is_first_chunk,
+                             void* C, void* stream);
 
 /* A5 + A6 + A7 fused -- W13 grouped GEMM with SiLU*up and 1x128 FP8 quant of
  * the intermediate in the epilogue.

@@ -38,10 +38,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "moe_align_max_padded": (ctypes.c_int64, [_i64, _i32, _i32]),
     "moe_align_workspace_bytes": (ctypes.c_int64, [_i64, _i32]),
     "moe_align_block_size": (ctypes.c_int, [_P, _i64, _i32, _i32, _P, _P, _P, _i64, _P, _P]),
+    "moe_align_block_size_mapped": (ctypes.c_int, [_P, _i64, _i32, _i32, _P, _P, _P, _P, _i64, _P, _P]),
     "moe_grouped_gemm": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32, _i64,
                                         _i64, _i32, _i32, _i64, _P, _P]),
     "moe_grouped_gemm_ordered": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32,
                                                 _i64, _i64, _i32, _i32, _i64, _i32, _P, _P]),
+    "moe_grouped_gemm_n_split": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32, _i64,
+                                                _i64, _i64, _i64, _i32, _i32, _i64, _P, _P]),
+    "moe_grouped_gemm_k_split": (ctypes.c_int, [_P, _P, _i64, _i64, _P, _P, _P, _P, _P, _P, _i64, _i32,
+                                                _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i64, _i32, _P,
+                                                _P]),
     "moe_silu_mul_quant_group128": (ctypes.c_int, [_P, _i64, _i64, _P, _P, _P]),
     "moe_reduce_topk_add": (ctypes.c_int, [_P, _P, _i64, _i32, _i64, _P, _P]),
     "moe_gemm_w13_silu_quant": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,

@@ -155,7 +155,8 @@ __global__ __launch_bounds__(kAlignMaxExperts) void align_scan_kernel(
 __global__ __launch_bounds__(256) void align_place_kernel(
     const int32_t* __restrict__ ids, int64_t S, int E, int BM, const int32_t* __restrict__ chunk_base,
     const int32_t* __restrict__ rank, const int32_t* __restrict__ off, const int32_t* __restrict__ cnt,
-    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids, int64_t max_padded) {
+    const int32_t* __restrict__ expert_map, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ expert_ids, int64_t max_padded) {
   __shared__ int32_t s_off[kAlignMaxExperts + 1];
   __shared__ int32_t s_cnt[kAlignMaxExperts];
   for (int i = threadIdx.x; i <= E; i += 256) s_off[i] = off[i];
@@ -184,7 +185,9 @@ __global__ __launch_bounds__(256) void align_place_kernel(
       pad = (i - s_off[e]) >= s_cnt[e];
     }
     if (pad) sorted_ids[i] = (int32_t)S;
-    if (i % BM == 0) expert_ids[i / BM] = e;
+    // With an expert map (global -> local id, -1 = not on this device) the
+    // block's expert is reported as its local id.
+    if (i % BM == 0) expert_ids[i / BM] = (expert_map && e >= 0) ? expert_map[e] : e;
   }
 }
 
@@ -206,9 +209,9 @@ extern "C" int64_t moe_align_workspace_bytes(int64_t S, int32_t E) {
   return 4 * (n_chunks * E + S + 2 * (int64_t)E + 1) + 256;
 }
 
-extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
-                                    int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
-                                    int64_t max_padded, void* workspace, void* stream) {
+static int align_impl(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM, const int32_t* expert_map,
+                      int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
+                      void* workspace, void* stream) {
   if (S < 0) return kErrBadShape;
   if (E <= 0 || E > kAlignMaxExperts) return kErrBadExperts;
   if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
@@ -244,8 +247,23 @@ extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t 
   const int64_t wide = S > max_padded ? S : max_padded;
   if (wide > 0) {
     hipLaunchKernelGGL(align_place_kernel, dim3((unsigned)((wide + 255) / 256)), dim3(256), 0, st,
-                       topk_ids, S, (int)E, (int)BM, chunk_count, rank, off, cnt, sorted_ids,
-                       expert_ids, max_padded);
+                       topk_ids, S, (int)E, (int)BM, chunk_count, rank, off, cnt, expert_map,
+                       sorted_ids, expert_ids, max_padded);
   }
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
+                                    int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
+                                    int64_t max_padded, void* workspace, void* stream) {
+  return align_impl(topk_ids, S, E, BM, nullptr, sorted_ids, expert_ids, ntpp, max_padded, workspace, stream);
+}
+
+extern "C" int moe_align_block_size_mapped(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
+                                           const int32_t* expert_map, int32_t* sorted_ids,
+                                           int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
+                                           void* workspace, void* stream) {
+  if (!expert_map) return kErrNullPointer;
+  return align_impl(topk_ids, S, E, BM, expert_map, sorted_ids, expert_ids, ntpp, max_padded, workspace,
+                    stream);
 }

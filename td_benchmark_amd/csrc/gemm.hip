@@ -123,7 +123,29 @@ struct GemmArgs {
   int a_by_pos;
   int E;
   int tile_order;          // 0 expert-major (XCD-contiguous), 1 shuffled, 2 half-phase
+  // Strides of the (possibly sliced) operands; base pointers are pre-offset.
+  int64_t lda;             // A row stride, bytes
+  int64_t as_ld;           // A_scale row stride, floats
+  int64_t ldb;             // B row stride, bytes
+  int64_t b_es;            // B expert stride, bytes
+  int64_t bs_ld;           // B_scale stride between 128-row groups, floats
+  int64_t bs_es;           // B_scale expert stride, floats
+  int64_t ldc;             // C row stride, elements (plain epilogue)
+  int accumulate;          // plain epilogue: C = bf16(C + bf16(result)) instead of C = bf16(result)
 };
+
+// Dense (unsliced) strides for A [rows, K], B [E, N, K], C [S, N].
+static inline void dense_strides(GemmArgs& g) {
+  const int64_t KB = g.K / 128;
+  g.lda = g.K;
+  g.as_ld = KB;
+  g.ldb = g.K;
+  g.b_es = g.N * g.K;
+  g.bs_ld = KB;
+  g.bs_es = (g.N / 128) * KB;
+  g.ldc = g.N;
+  g.accumulate = 0;
+}
 
 // Chunk swizzle of an LDS row (see the header comment).
 MOE_HOST_DEVICE int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
@@ -272,6 +294,7 @@ void grouped_gemm_kernel(GemmArgs g) {
       for (int row = tid; row < BM; row += T::THREADS)
         g.hs[(b * BM + row) * (g.I / 128) + j] = kScaleFloor;
     } else {
+      if (g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
       for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
         const int row = ci >> 5, cc = ci & 31;
         const int64_t slot = g.sorted[b * BM + row];
@@ -279,7 +302,7 @@ void grouped_gemm_kernel(GemmArgs g) {
         const int grp = cc >> 4;
         if (grp == 1 && !g1_store) continue;
         const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
-        *reinterpret_cast<v4i*>(g.C + slot * g.N + n) = (v4i){0, 0, 0, 0};
+        *reinterpret_cast<v4i*>(g.C + slot * g.ldc + n) = (v4i){0, 0, 0, 0};
       }
     }
     return;
@@ -313,7 +336,7 @@ void grouped_gemm_kernel(GemmArgs g) {
     const int gi = wave + T::NW * i;
     const int row = (gi < T::NA) ? 8 * gi + (lane >> 3) : 0;
     const int cc = slot_of(lane & 7, row);
-    a_off[i] = (uint32_t)(a_row_of(row) * K) + (uint32_t)(cc * 16);
+    a_off[i] = (uint32_t)(a_row_of(row) * g.lda) + (uint32_t)(cc * 16);
   }
   // B instruction gi = wave + 4*i (i < 8) covers B-tile rows 8*gi .. 8*gi+7;
   // tile rows 0..127 are scale group g0, rows 128..255 group g1.  The lane's
@@ -324,17 +347,17 @@ void grouped_gemm_kernel(GemmArgs g) {
   {
     const int r0 = 8 * wave + (lane >> 3);
     const int cc = slot_of(lane & 7, r0);
-    b_off = (uint32_t)(r0 * K) + (uint32_t)(cc * 16);
+    b_off = (uint32_t)(r0 * g.ldb) + (uint32_t)(cc * 16);
   }
   // A scales: instruction s (issued by wave NW-1-s) covers rows 64*s .. 64*s+63.
   const int s_idx = T::NW - 1 - wave;
   uint32_t sa_off = 0;
   if (s_idx < T::NS) {
     const int row = 64 * s_idx + lane;
-    sa_off = (uint32_t)(a_row_of(row < BM ? row : 0) * KB) * 4u;
+    sa_off = (uint32_t)(a_row_of(row < BM ? row : 0) * g.as_ld) * 4u;
   }
-  const uint8_t* b_grp0 = g.B + ((int64_t)e * g.N + g0 * 128) * K;
-  const uint8_t* b_grp1 = g.B + ((int64_t)e * g.N + g1 * 128) * K;
+  const uint8_t* b_grp0 = g.B + (int64_t)e * g.b_es + g0 * 128 * g.ldb;
+  const uint8_t* b_grp1 = g.B + (int64_t)e * g.b_es + g1 * 128 * g.ldb;
 
   auto issue_stage = [&](int kk, int stage) {
     uint8_t* dst = smem + stage * T::STAGE;
@@ -349,7 +372,7 @@ void grouped_gemm_kernel(GemmArgs g) {
     constexpr int HALF = T::NB_W / 2;
 #pragma unroll
     for (int i = 0; i < T::NB_W; ++i) {
-      const uint8_t* bbase = (i < HALF ? b_grp0 : b_grp1) + (int64_t)(8 * T::NW * (i % HALF)) * K + kk * 128;
+      const uint8_t* bbase = (i < HALF ? b_grp0 : b_grp1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
       dma16(bbase + b_off, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
     }
     if (s_idx < T::NS)
@@ -360,7 +383,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   // Weight scales of both groups for every K block (read once, plain loads).
   for (int i = tid; i < 2 * KB; i += T::THREADS) {
     const int grp = i / KB, kk = i % KB;
-    smSB[grp * kMaxKB + kk] = g.Bs[((int64_t)e * NBt + (grp ? g1 : g0)) * KB + kk];
+    smSB[grp * kMaxKB + kk] = g.Bs[(int64_t)e * g.bs_es + (grp ? g1 : g0) * g.bs_ld + kk];
   }
 
   v4f acc[T::RS][2][T::CS];
@@ -564,8 +587,19 @@ void grouped_gemm_kernel(GemmArgs g) {
       const int grp = cc >> 4;
       if (grp == 1 && !g1_store) continue;
       const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
-      *reinterpret_cast<v4i*>(g.C + slot * g.N + n) =
-          *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
+      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
+      v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
+      if (g.accumulate) {
+        // K-split accumulation: the bf16 partial is added to the bf16 C of the
+        // earlier chunks and rounded again.
+        const v4i old = *dst;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
+          val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
+        }
+      }
+      *dst = val;
     }
   }
 }
@@ -650,6 +684,7 @@ extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, con
   g.a_by_pos = a_by_pos ? 1 : 0;
   g.E = E;
   g.tile_order = tile_order;
+  dense_strides(g);
   return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
 }
 
@@ -662,6 +697,103 @@ extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void*
   return moe_grouped_gemm_ordered(A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp,
                                   topk_weights, S, top_k, a_by_pos, N, K, E, BM, max_padded, 0, C,
                                   stream);
+}
+
+// Shared argument checks and setup of the plain-epilogue GEMM on (possibly
+// sliced) operands; the caller fills the strides and pre-offsets the bases.
+static int setup_plain(GemmArgs& g, const void* A, const float* A_scale, const void* B, const float* B_scale,
+                       const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                       const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos, int64_t N,
+                       int64_t K, int32_t E, int32_t BM, int64_t max_padded, void* C) {
+  if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
+  if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
+  if (top_k <= 0) return kErrBadTopK;
+  if (E <= 0) return kErrBadExperts;
+  if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
+    return kErrNullPointer;
+  g = GemmArgs{};
+  g.A = (const uint8_t*)A;
+  g.As = A_scale;
+  g.B = (const uint8_t*)B;
+  g.Bs = B_scale;
+  g.sorted = sorted_ids;
+  g.eids = expert_ids;
+  g.ntpp = ntpp;
+  g.topk_w = topk_weights;
+  g.C = (uint16_t*)C;
+  g.S = S;
+  g.N = N;
+  g.K = K;
+  g.max_blocks = (max_padded + BM - 1) / BM;
+  g.n_tiles = (N / 128 + 1) / 2;
+  g.top_k = top_k;
+  g.a_by_pos = a_by_pos ? 1 : 0;
+  g.E = E;
+  dense_strides(g);
+  return kOk;
+}
+
+extern "C" int moe_grouped_gemm_n_split(const void* A, const float* A_scale, const void* B,
+                                        const float* B_scale, const int32_t* sorted_ids,
+                                        const int32_t* expert_ids, const int32_t* ntpp,
+                                        const float* topk_weights, int64_t S, int32_t top_k,
+                                        int32_t a_by_pos, int64_t full_N, int64_t N_offset,
+                                        int64_t N_chunk, int64_t K, int32_t E, int32_t BM,
+                                        int64_t max_padded, void* C, void* stream) {
+  if (full_N <= 0 || N_offset < 0 || N_chunk <= 0 || N_offset + N_chunk > full_N) return kErrBadShape;
+  if (full_N % 128 != 0 || N_offset % 128 != 0) return kErrBadShape;
+  GemmArgs g;
+  const int rc = setup_plain(g, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, top_k,
+                             a_by_pos, N_chunk, K, E, BM, max_padded, C);
+  if (rc != kOk || max_padded == 0 || S == 0) return rc;
+  const int64_t KB = K / 128;
+  // B[:, N_offset:N_offset+N_chunk, :], B_scale[:, N_offset/128:, :], C[:, N_offset:]
+  g.B += N_offset * K;
+  g.Bs += (N_offset / 128) * KB;
+  g.C += N_offset;
+  g.b_es = full_N * K;
+  g.bs_es = (full_N / 128) * KB;
+  g.ldc = full_N;
+  if (!aligned16(g.A) || !aligned16(g.B) || !aligned16(g.C)) return kErrBadShape;
+  const int64_t a_rows = a_by_pos ? max_padded : (S + top_k - 1) / top_k;
+  if (!offsets_fit(a_rows, full_N, K)) return kErrBadShape;
+  return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int64_t A_cols,
+                                        int64_t A_K_offset, const void* B, const float* B_scale,
+                                        const int32_t* sorted_ids, const int32_t* expert_ids,
+                                        const int32_t* ntpp, const float* topk_weights, int64_t S,
+                                        int32_t top_k, int32_t a_by_pos, int64_t N, int64_t full_K,
+                                        int64_t K_offset, int64_t K_chunk, int32_t E, int32_t BM,
+                                        int64_t max_padded, int32_t is_first_chunk, void* C,
+                                        void* stream) {
+  if (full_K <= 0 || K_offset < 0 || K_chunk <= 0 || K_offset + K_chunk > full_K) return kErrBadShape;
+  if (A_cols <= 0 || A_K_offset < 0 || A_K_offset + K_chunk > A_cols) return kErrBadShape;
+  if (full_K % 128 != 0 || K_offset % 128 != 0 || A_cols % 128 != 0 || A_K_offset % 128 != 0)
+    return kErrBadShape;
+  GemmArgs g;
+  const int rc = setup_plain(g, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, top_k,
+                             a_by_pos, N, K_chunk, E, BM, max_padded, C);
+  if (rc != kOk || max_padded == 0 || S == 0) return rc;
+  // A[:, A_K_offset:+K_chunk] of an [rows, A_cols] tensor (scales [rows, A_cols/128]),
+  // B[:, :, K_offset:+K_chunk] of [E, N, full_K] (scales [E, N/128, full_K/128]).
+  g.A += A_K_offset;
+  g.As += A_K_offset / 128;
+  g.lda = A_cols;
+  g.as_ld = A_cols / 128;
+  g.B += K_offset;
+  g.Bs += K_offset / 128;
+  g.ldb = full_K;
+  g.b_es = N * full_K;
+  g.bs_ld = full_K / 128;
+  g.bs_es = (N / 128) * (full_K / 128);
+  g.accumulate = is_first_chunk ? 0 : 1;
+  if (!aligned16(g.A) || !aligned16(g.B) || !aligned16(g.C)) return kErrBadShape;
+  const int64_t a_rows = a_by_pos ? max_padded : (S + top_k - 1) / top_k;
+  if (!offsets_fit(a_rows, N, full_K) || a_rows * A_cols >= ((int64_t)1 << 32)) return kErrBadShape;
+  return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
 }
 
 extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,
@@ -700,6 +832,7 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
   g.top_k = top_k;
   g.a_by_pos = 0;
   g.E = E;
+  dense_strides(g);
   return dispatch_gemm<true>(BM, g, (hipStream_t)stream);
 }
 

@@ -116,13 +116,25 @@ class AlignBuffers:
         self.workspace = torch.empty(align_workspace_bytes(num_slots, num_experts), dtype=torch.uint8,
                                      device=device)
 
-    def run(self, topk_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    def run(self, topk_ids: torch.Tensor,
+            expert_map: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """``expert_map`` (int32 [E], global -> local expert id or -1): block
+        expert ids are reported as local ids (expert parallelism)."""
         _need(topk_ids, "topk_ids", torch.int32)
         if topk_ids.numel() != self.S:
             raise ValueError(f"topk_ids has {topk_ids.numel()} slots, buffers were sized for {self.S}")
-        check(lib().moe_align_block_size(_ptr(topk_ids), self.S, self.E, self.BM, _ptr(self.sorted_ids),
-                                         _ptr(self.expert_ids), _ptr(self.ntpp), self.max_padded,
-                                         _ptr(self.workspace), _stream()), "moe_align_block_size")
+        if expert_map is None:
+            check(lib().moe_align_block_size(_ptr(topk_ids), self.S, self.E, self.BM, _ptr(self.sorted_ids),
+                                             _ptr(self.expert_ids), _ptr(self.ntpp), self.max_padded,
+                                             _ptr(self.workspace), _stream()), "moe_align_block_size")
+        else:
+            _need(expert_map, "expert_map", torch.int32)
+            if expert_map.numel() != self.E:
+                raise ValueError(f"expert_map must have {self.E} entries")
+            check(lib().moe_align_block_size_mapped(_ptr(topk_ids), self.S, self.E, self.BM, _ptr(expert_map),
+                                                    _ptr(self.sorted_ids), _ptr(self.expert_ids), _ptr(self.ntpp),
+                                                    self.max_padded, _ptr(self.workspace), _stream()),
+                  "moe_align_block_size_mapped")
         return self.sorted_ids[: self.max_padded], self.expert_ids[: self.max_blocks], self.ntpp
 
 
@@ -130,11 +142,12 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
                          expert_map: torch.Tensor | None = None):
     """vLLM's moe_align_block_size(topk_ids, BM, E, expert_map) as called at
     overlap/overlap_forward.py:165-169 -> (sorted_token_ids, expert_ids,
-    num_tokens_post_padded).  Stable order within each expert, pad value S."""
-    if expert_map is not None:
-        raise NotImplementedError("expert_map (expert parallelism) is outside the single-GPU path")
+    num_tokens_post_padded).  Stable order within each expert, pad value S.
+    With ``expert_map`` the E global experts are sorted and padded and the
+    block expert ids become local ids (-1 for experts not on this device)."""
     bufs = AlignBuffers(topk_ids.numel(), num_experts, block_size, topk_ids.device)
-    return bufs.run(topk_ids.contiguous())
+    em = None if expert_map is None else expert_map.to(torch.int32).contiguous()
+    return bufs.run(topk_ids.contiguous().view(-1), em)
 
 
 # ---------------------------------------------------------------------------
@@ -178,6 +191,77 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                                          _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
                                          1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(),
                                          int(tile_order), _ptr(C), _stream()), "moe_grouped_gemm")
+
+
+def invoke_moe_kernel_n_split(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, A_scale: torch.Tensor,
+                              B_scale: torch.Tensor, B_zp: Any, topk_weights: torch.Tensor | None,
+                              sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
+                              num_tokens_post_padded: torch.Tensor, mul_routed_weight: bool, top_k: int,
+                              config: dict | None, compute_type: Any = None, use_fp8_w8a8: bool = True,
+                              use_int8_w8a8: bool = False, use_int8_w8a16: bool = False,
+                              use_int4_w4a16: bool = False, per_channel_quant: bool = False,
+                              N_offset: int = 0, N_chunk: int | None = None,
+                              block_shape: list[int] | None = None, B_bias: Any = None,
+                              a_by_pos: bool = False) -> None:
+    """The reference's N-split grouped GEMM (overlap/kernels.py:219-310):
+    C[..., N_offset:N_offset+N_chunk] from the matching rows of B and groups
+    of B_scale.  C is [M, top_k, full_N] or [S, 1, full_N] (rows by slot)."""
+    if not use_fp8_w8a8 or use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or per_channel_quant:
+        raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
+    if B_zp is not None or B_bias is not None:
+        raise NotImplementedError("zero points / bias are not on this path")
+    if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
+        raise NotImplementedError("only block_shape [128,128]")
+    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
+                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
+        _need(t, name)
+    E, full_N, K = B.shape
+    N_chunk = full_N - N_offset if N_chunk is None else N_chunk
+    S = C.numel() // full_N
+    BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
+    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
+    if mul_routed_weight and topk_weights is None:
+        raise ValueError("mul_routed_weight requires topk_weights")
+    check(lib().moe_grouped_gemm_n_split(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids),
+                                         _ptr(expert_ids), _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
+                                         1 if a_by_pos else 0, full_N, N_offset, N_chunk, K, E, BM,
+                                         sorted_token_ids.numel(), _ptr(C), _stream()), "moe_grouped_gemm_n_split")
+
+
+def invoke_moe_kernel_k_split(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, A_scale: torch.Tensor,
+                              B_scale: torch.Tensor, topk_weights: torch.Tensor | None,
+                              sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
+                              num_tokens_post_padded: torch.Tensor, mul_routed_weight: bool, top_k: int,
+                              config: dict | None, compute_type: Any = None, use_fp8_w8a8: bool = True,
+                              use_int8_w8a8: bool = False, per_channel_quant: bool = False,
+                              K_offset: int = 0, K_chunk: int | None = None, is_first_chunk: bool = True,
+                              block_shape: list[int] | None = None, A_K_offset: int = -1,
+                              a_by_pos: bool = False) -> None:
+    """The reference's K-split accumulate GEMM (overlap/kernels.py:317-452):
+    the partial product over A[:, A_K_offset:+K_chunk] and
+    B[:, :, K_offset:+K_chunk] is stored into C on the first chunk and added
+    to it (bf16) afterwards.  A_K_offset = -1 means K_offset (A and B sliced
+    alike); 0 means A already is the K sub-range."""
+    if not use_fp8_w8a8 or use_int8_w8a8 or per_channel_quant:
+        raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
+    if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
+        raise NotImplementedError("only block_shape [128,128]")
+    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
+                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
+        _need(t, name)
+    E, N, full_K = B.shape
+    K_chunk = full_K - K_offset if K_chunk is None else K_chunk
+    a_k = K_offset if A_K_offset < 0 else A_K_offset
+    S = C.numel() // N
+    BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
+    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
+    if mul_routed_weight and topk_weights is None:
+        raise ValueError("mul_routed_weight requires topk_weights")
+    check(lib().moe_grouped_gemm_k_split(_ptr(A), _ptr(A_scale), A.shape[-1], a_k, _ptr(B), _ptr(B_scale),
+                                         _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(num_tokens_post_padded),
+                                         _ptr(w), S, top_k, 1 if a_by_pos else 0, N, full_K, K_offset, K_chunk,
+                                         E, BM, sorted_token_ids.numel(), 1 if is_first_chunk else 0, _ptr(C),
+                                         _stream()), "moe_grouped_gemm_k_split")
 
 
 def _block_m_from(sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor) -> int:
@@ -362,7 +446,8 @@ class FusedExpertsRunner:
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
-                 shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None):
+                 shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None,
+                 global_num_experts: int | None = None, expert_map: torch.Tensor | None = None):
         for name, t in (("w13", w13), ("w2", w2)):
             _need(t, name, FP8)
         _need(w13_scale, "w13_scale", torch.float32)
@@ -383,7 +468,18 @@ class FusedExpertsRunner:
         dev = w13.device
         self.q1 = torch.empty((self.T, H), dtype=FP8, device=dev)
         self.s1 = torch.empty((self.T, H // 128), dtype=torch.float32, device=dev)
-        self.align = AlignBuffers(self.S, E, self.BM, dev)
+        # Expert parallelism: align over the global experts, GEMMs over the
+        # local ones (blocks of non-local experts are -1 and produce zeros).
+        self.expert_map = None
+        n_align = E
+        if expert_map is not None:
+            self.expert_map = expert_map.to(device=dev, dtype=torch.int32).contiguous()
+            n_align = int(global_num_experts or self.expert_map.numel())
+            if self.expert_map.numel() != n_align:
+                raise ValueError("expert_map must have global_num_experts entries")
+        elif global_num_experts not in (None, -1, E):
+            raise ValueError("global_num_experts != local experts needs an expert_map")
+        self.align = AlignBuffers(self.S, n_align, self.BM, dev)
         mp = max(self.align.max_padded, 1)
         self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
         self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
@@ -402,7 +498,7 @@ class FusedExpertsRunner:
                                        _stream()), "moe_quant_group128")
 
     def stage_align(self, topk_ids: torch.Tensor) -> None:
-        self.align.run(topk_ids)
+        self.align.run(topk_ids, self.expert_map)
 
     def stage_w13(self) -> None:
         a = self.align
@@ -487,19 +583,23 @@ class ChunkedExpertsRunner:
 def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                   topk_weights: torch.Tensor, topk_ids: torch.Tensor, global_num_experts: int = -1,
                   w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
-                  block_size_m: int | None = None, quant_config: Any = None) -> torch.Tensor:
+                  block_size_m: int | None = None, quant_config: Any = None,
+                  expert_map: torch.Tensor | None = None) -> torch.Tensor:
     """vLLM ``fused_experts`` as the reference calls it (schemes/vllm_tp.py:
-    189-197) for FP8 w8a8 with [128,128] weight blocks.  Scales come either as
+    52-60; with ``expert_map`` for expert parallelism, schemes/vllm_ep.py:
+    57-66) for FP8 w8a8 with [128,128] weight blocks.  Scales come either as
     keywords or from ``quant_config`` (attributes ``w1_scale``/``w2_scale``).
-    Allocates per call; prebuild a FusedExpertsRunner for timed loops."""
+    With an expert map, w1/w2 hold the local experts and slots routed to other
+    devices contribute zeros.  Allocates per call; prebuild a
+    FusedExpertsRunner for timed loops."""
     if quant_config is not None:
         w1_scale = getattr(quant_config, "w1_scale", w1_scale)
         w2_scale = getattr(quant_config, "w2_scale", w2_scale)
     if w1_scale is None or w2_scale is None:
         raise ValueError("fused_experts needs w1_scale and w2_scale")
-    if global_num_experts not in (-1, w1.shape[0]):
-        raise NotImplementedError("global_num_experts != local experts needs an expert_map")
     T, k = topk_ids.shape
-    runner = FusedExpertsRunner(w1, w1_scale, w2, w2_scale, T, k, block_size_m)
+    gne = None if global_num_experts in (-1, None) else global_num_experts
+    runner = FusedExpertsRunner(w1, w1_scale, w2, w2_scale, T, k, block_size_m,
+                                global_num_experts=gne, expert_map=expert_map)
     return runner.run(hidden_states.contiguous(), topk_weights.contiguous().view(-1),
                       topk_ids.contiguous().view(-1)).clone()

@@ -1,0 +1,182 @@
+"""GPU parity of the chunked GEMM modes and of the expert map.
+
+N-split (overlap/kernels.py:219-310): the column chunks, assembled, equal the
+one-shot GEMM bit for bit (every output element is computed the same way).
+K-split (overlap/kernels.py:317-452): the first chunk over a K window equals
+the one-shot GEMM on that window bit for bit, and the accumulated chunks match
+the oracle's composition of per-chunk bf16 partials,
+C = bf16(C + bf16(partial)), within the FP8-MFMA accumulation bound; expert -1
+rows are written on the first chunk only.  Expert map (vLLM
+moe_align_block_size with expert_map): align over global experts with local
+block ids gives the same layer output, bit for bit, as the local-only problem
+in which non-local slots are dropped."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from moe_cases import bf16_bits, make_case, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(T=150, H=512, I=384, E=6, k=3, BM=32, seed=21):
+    import torch
+
+    from td_benchmark_amd import ops
+
+    c = make_case(T=T, H=H, I=I, E=E, k=k, BM=BM, seed=seed)
+    g = to_gpu(c)
+    q, s = ops.per_token_group_quant_fp8(g["x"])
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(g["topk_ids"].view(-1), BM, E)
+    torch.cuda.synchronize()
+    return c, g, q, s, sorted_ids, eids, ntpp
+
+
+@pytest.mark.parametrize("chunks", [[128, 256, 384], [384, 384], [768]])
+def test_n_split_assembles_the_full_gemm(chunks):
+    import torch
+
+    from td_benchmark_amd import ops
+
+    print(f"case: n_split {chunks}", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup()
+    N = 2 * c.I
+    assert sum(chunks) == N
+    full = torch.zeros((c.S, N), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(q, g["w13"], full, s, g["w13_s"], None, None, sorted_ids, eids, ntpp, False, c.k,
+                                  {"BLOCK_SIZE_M": c.BM})
+    parts = torch.full((c.S, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    off = 0
+    for n in chunks:
+        ops.invoke_moe_kernel_n_split(q, g["w13"], parts, s, g["w13_s"], None, None, sorted_ids, eids, ntpp, False,
+                                      c.k, {"BLOCK_SIZE_M": c.BM}, N_offset=off, N_chunk=n)
+        off += n
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(parts), bf16_bits(full))
+
+
+def test_n_split_w2_routed_rows_by_position():
+    import torch
+
+    from td_benchmark_amd import ops
+
+    print("case: n_split W2", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup(H=768, I=256)
+    hq, hs = ops.gemm_w13_silu_quant(q, s, g["w13"], g["w13_s"], sorted_ids, eids, ntpp, c.S, c.k, c.BM)
+    w = g["topk_w"].view(-1)
+    full = torch.zeros((c.S, c.H), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(hq, g["w2"], full, hs, g["w2_s"], None, w, sorted_ids, eids, ntpp, True, 1,
+                                  {"BLOCK_SIZE_M": c.BM}, a_by_pos=True)
+    parts = torch.zeros_like(full)
+    for off in (0, 256, 512):
+        ops.invoke_moe_kernel_n_split(hq, g["w2"], parts, hs, g["w2_s"], None, w, sorted_ids, eids, ntpp, True, 1,
+                                      {"BLOCK_SIZE_M": c.BM}, N_offset=off, N_chunk=256, a_by_pos=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(parts), bf16_bits(full))
+
+
+@pytest.mark.parametrize("bounds", [[0, 256, 512], [0, 128, 384, 512], [0, 512]])
+def test_k_split_accumulates_like_the_reference(bounds):
+    import torch
+
+    from td_benchmark_amd import ops
+
+    print(f"case: k_split {bounds}", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup()
+    eids_masked = eids.clone()
+    eids_masked[1] = -1                      # a non-local block: zeros on the first chunk only
+    N = 2 * c.I
+    C = torch.full((c.S, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    for i, (k0, k1) in enumerate(zip(bounds[:-1], bounds[1:])):
+        ops.invoke_moe_kernel_k_split(q, g["w13"], C, s, g["w13_s"], None, sorted_ids, eids_masked, ntpp, False,
+                                      c.k, {"BLOCK_SIZE_M": c.BM}, K_offset=k0, K_chunk=k1 - k0,
+                                      is_first_chunk=(i == 0))
+    torch.cuda.synchronize()
+    got = bf16_bits(C)
+    # oracle composition over the same chunks
+    q_np = q.view(torch.uint8).cpu().numpy()
+    s_np = s.cpu().numpy()
+    srt, ei = sorted_ids.cpu().numpy(), eids_masked.cpu().numpy()
+    nt = int(ntpp.item())
+    ref = None
+    mag = np.zeros((c.S, N), np.float64)
+    abs_parts = np.zeros((c.S, N), np.float64)
+    for k0, k1 in zip(bounds[:-1], bounds[1:]):
+        part, m = oracle.grouped_gemm(q_np[:, k0:k1], s_np[:, k0 // 128:k1 // 128], c.w13_q[:, :, k0:k1],
+                                      c.w13_s[:, :, k0 // 128:k1 // 128], srt, ei, nt, c.BM, c.S, c.k,
+                                      with_magnitude=True)
+        mag += m
+        abs_parts += np.abs(oracle.bf16_to_f32(part))
+        ref = part if ref is None else oracle.f32_to_bf16(oracle.bf16_to_f32(ref) + oracle.bf16_to_f32(part))
+    g32, r32 = oracle.bf16_to_f32(got).astype(np.float64), oracle.bf16_to_f32(ref).astype(np.float64)
+    # rows of the masked block and of never-placed slots: zeros from the first chunk
+    placed = srt[:nt][(srt[:nt] < c.S)]
+    in_masked = srt[c.BM:2 * c.BM]
+    in_masked = in_masked[in_masked < c.S]
+    assert np.all(g32[in_masked] == 0.0)
+    # each chunk's partial may round to a neighbouring bf16 value (one ulp of
+    # the partial), and every accumulation rounds once more
+    tol = 2.0 ** -7 * (np.abs(r32) + abs_parts) + oracle.MFMA_L1_REL * mag + 1e-30
+    bad = np.abs(g32 - r32) > tol
+    assert not bad[placed].any(), f"{bad[placed].sum()} outputs outside the bound"
+
+
+def test_k_split_first_chunk_with_presliced_a_equals_window_gemm():
+    import torch
+
+    from td_benchmark_amd import ops
+
+    print("case: k_split A_K_offset=0", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup()
+    k0, k1 = 128, 384
+    q_sub = q.view(torch.uint8)[:, k0:k1].contiguous().view(ops.FP8)
+    s_sub = s[:, k0 // 128:k1 // 128].contiguous()
+    C = torch.zeros((c.S, 2 * c.I), dtype=torch.bfloat16, device="cuda")
+    ops.invoke_moe_kernel_k_split(q_sub, g["w13"], C, s_sub, g["w13_s"], None, sorted_ids, eids, ntpp, False, c.k,
+                                  {"BLOCK_SIZE_M": c.BM}, K_offset=k0, K_chunk=k1 - k0, is_first_chunk=True,
+                                  A_K_offset=0)
+    w_sub = g["w13"].view(torch.uint8)[:, :, k0:k1].contiguous().view(ops.FP8)
+    ws_sub = g["w13_s"][:, :, k0 // 128:k1 // 128].contiguous()
+    ref = torch.zeros_like(C)
+    ops.dispatch_fused_moe_kernel(q_sub, w_sub, ref, s_sub, ws_sub, None, None, sorted_ids, eids, ntpp, False, c.k,
+                                  {"BLOCK_SIZE_M": c.BM})
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(C), bf16_bits(ref))
+
+
+def test_expert_map_equals_local_problem():
+    import torch
+
+    from td_benchmark_amd import ops
+
+    print("case: expert_map", flush=True)
+    c = make_case(T=200, H=256, I=256, E=8, k=2, BM=16, seed=33)
+    local = [2, 5, 6]
+    emap = np.full(c.E, -1, np.int32)
+    emap[local] = np.arange(len(local), dtype=np.int32)
+    g = to_gpu(c)
+    w13 = g["w13"][local].contiguous()
+    w13_s = g["w13_s"][local].contiguous()
+    w2 = g["w2"][local].contiguous()
+    w2_s = g["w2_s"][local].contiguous()
+    em = torch.from_numpy(emap).cuda()
+    y_ep = ops.fused_experts(g["x"], w13, w2, g["topk_w"], g["topk_ids"], global_num_experts=c.E,
+                             w1_scale=w13_s, w2_scale=w2_s, block_size_m=16, expert_map=em)
+    # the local problem: slots of other devices dropped (their W2 rows stay
+    # zero, as the expert -1 blocks of the mapped path write them)
+    ids_local = torch.from_numpy(emap[c.topk_ids]).cuda()
+    loc = ops.FusedExpertsRunner(w13, w13_s, w2, w2_s, c.T, c.k, 16)
+    loc.D.zero_()
+    y_loc = loc.run(g["x"], g["topk_w"].view(-1), ids_local.view(-1))
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(y_ep), bf16_bits(y_loc))
+    # and the block ids are local ids (or -1)
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(g["topk_ids"], 16, c.E, expert_map=em)
+    torch.cuda.synchronize()
+    _, eids_ref, ntpp_ref = oracle.moe_align(c.topk_ids, c.E, 16)
+    nb = ntpp_ref // 16
+    assert int(ntpp.item()) == ntpp_ref
+    mapped = np.where(eids_ref[:nb] >= 0, emap[np.maximum(eids_ref[:nb], 0)], -1)
+    assert np.array_equal(eids.cpu().numpy()[:nb], mapped)
