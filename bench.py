@@ -177,6 +177,20 @@ def main() -> int:
     ms_single = ms_per_step
     stage_ms = {name: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
                 for j, name in enumerate(STAGES)}
+    # The same layer replayed from a captured HIP graph (one launch per step);
+    # shows the launch overhead that matters for the small configurations.
+    ms_graph = None
+    if pipe is None:
+        graph = runner.capture(data.x, data.topk_w, data.topk_ids)
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms_graph = start.elapsed_time(end) / args.steps
     if pipe is not None:
         for _ in range(args.warmup):
             pipe.run(data.x, data.topk_w, data.topk_ids)
@@ -240,6 +254,7 @@ def main() -> int:
                    "parallelism": "single GPU, all experts local"},
         "layer_us": ms_per_step * 1e3,
         "layer_us_single_pass": ms_single * 1e3,
+        "layer_us_graph": None if ms_graph is None else ms_graph * 1e3,
         "gemm_tflops": wl.gemm_flop / (gemm_ms / 1e3) / 1e12,
         "gemm_mfma_frac": wl.gemm_flop / (gemm_ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS,
         "stages": stages,

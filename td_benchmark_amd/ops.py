@@ -534,6 +534,34 @@ class FusedExpertsRunner:
         self.stage_reduce()
         return self.y
 
+    def capture(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> "LayerGraph":
+        """Record the layer's launches once into a HIP graph bound to these
+        input tensors; ``LayerGraph.replay()`` then re-runs the whole layer
+        with one launch (new inputs go into the same tensors).  The layer's
+        kernels take every size from their arguments and clear nothing with a
+        memset, so a replay equals an eager run."""
+        return LayerGraph(self, hidden, topk_weights, topk_ids)
+
+
+class LayerGraph:
+    """A captured FusedExpertsRunner.run (see FusedExpertsRunner.capture)."""
+
+    def __init__(self, runner: "FusedExpertsRunner", hidden: torch.Tensor, topk_weights: torch.Tensor,
+                 topk_ids: torch.Tensor):
+        self.runner, self.inputs = runner, (hidden, topk_weights, topk_ids)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            runner.run(*self.inputs)  # first calls set kernel attributes outside the capture
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            runner.run(*self.inputs)
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.runner.y
+
 
 class ChunkedExpertsRunner:
     """The layer over ``n_chunks`` token chunks pipelined on ``n_streams`` HIP

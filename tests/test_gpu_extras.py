@@ -218,3 +218,34 @@ def test_microbench_writes_measured_rows(name, tmp_path):
         assert r["status"] == "MEASURED"
         assert len(r["samples_ms"]) == 2
         assert r["metrics"]["latency_ms"] > 0
+
+
+def test_layer_graph_replays_equal_eager_runs():
+    torch = _torch()
+    from td_benchmark_amd import ops
+
+    print("case: layer graph replay", flush=True)
+    c = make_case(T=120, H=256, I=256, E=8, k=2, BM=32, seed=44)
+    c2 = make_case(T=120, H=256, I=256, E=8, k=2, BM=32, seed=45)
+    g, g2 = to_gpu(c), to_gpu(c2)
+    eager = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 32)
+    y_ref = bf16_bits(eager.run(g["x"], g["topk_w"].view(-1), g["topk_ids"].view(-1)))
+    y_ref2 = bf16_bits(eager.run(g2["x"], g2["topk_w"].view(-1), g2["topk_ids"].view(-1)))
+    runner = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 32)
+    x, w, ids = g["x"].clone(), g["topk_w"].view(-1).clone(), g["topk_ids"].view(-1).clone()
+    graph = runner.capture(x, w, ids)
+    for i in range(3):
+        # unrelated eager work and a host synchronisation between replays
+        junk = torch.randn(512, 512, device="cuda") @ torch.randn(512, 512, device="cuda")
+        torch.cuda.synchronize()
+        y = graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(y), y_ref), f"replay {i}"
+        del junk
+    # new inputs through the captured tensors
+    x.copy_(g2["x"])
+    w.copy_(g2["topk_w"].view(-1))
+    ids.copy_(g2["topk_ids"].view(-1))
+    y = graph.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(y), y_ref2)
