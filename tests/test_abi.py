@@ -92,3 +92,28 @@ def test_validation_rejects_bad_arguments_without_device_work(L):
     # empty problems are a no-op success
     assert L.moe_reduce_topk(None, 0, 8, 128, None, None) == 0
     assert L.moe_quant_group128(None, 0, 128, None, None, None) == 0
+
+
+def test_chunked_and_mapped_entry_points_validate_arguments(L):
+    E = {name: code for code, name in _lib.STATUS.items()}
+    buf = (ctypes.c_int32 * 64)()          # host memory: only ever passed to a rejected call
+    d = ctypes.cast(buf, ctypes.c_void_p)
+    # N-split: the window must lie inside full_N and start on a 128 boundary
+    args = [d, d, d, d, d, d, d, None, 10, 2, 0]
+    assert L.moe_grouped_gemm_n_split(*args, 512, 384, 256, 256, 4, 64, 100, d, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_grouped_gemm_n_split(*args, 512, 64, 128, 256, 4, 64, 100, d, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_grouped_gemm_n_split(None, None, None, None, None, None, None, None, 10, 2, 0, 512, 128, 128,
+                                      256, 4, 64, 100, None, None) == E["MOE_ERR_NULL_POINTER"]
+    assert L.moe_grouped_gemm_n_split(*args, 512, 128, 128, 256, 4, 48, 100, d, None) == E["MOE_ERR_BAD_BLOCK_SIZE"]
+    # K-split: the K window must lie inside both A and B
+    kargs = [d, d, 512, 0, d, d, d, d, d, None, 10, 2, 0, 256]
+    assert L.moe_grouped_gemm_k_split(*kargs, 512, 384, 256, 4, 64, 100, 1, d, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_grouped_gemm_k_split(d, d, 256, 128, d, d, d, d, d, None, 10, 2, 0, 256, 512, 0, 256, 4, 64,
+                                      100, 1, d, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_grouped_gemm_k_split(*kargs, 512, 64, 128, 4, 64, 100, 1, d, None) == E["MOE_ERR_BAD_SHAPE"]
+    # mapped align needs its map
+    assert L.moe_align_block_size_mapped(d, 10, 4, 16, None, d, d, d, 100, d, None) == E["MOE_ERR_NULL_POINTER"]
+    assert L.moe_align_block_size_mapped(d, 10, 4, 16, d, d, d, d, 10, d, None) == E["MOE_ERR_CAPACITY"]
+    # tile order out of range
+    assert L.moe_grouped_gemm_ordered(d, d, d, d, d, d, d, None, 10, 2, 0, 256, 256, 4, 64, 100, 3, d,
+                                      None) == E["MOE_ERR_BAD_SHAPE"]
