@@ -146,13 +146,14 @@ def test_k_split_first_chunk_with_presliced_a_equals_window_gemm():
     assert np.array_equal(bf16_bits(C), bf16_bits(ref))
 
 
-def test_expert_map_equals_local_problem():
+@pytest.mark.parametrize("T", [200, 700])   # one-launch and three-launch align paths
+def test_expert_map_equals_local_problem(T):
     import torch
 
     from td_benchmark_amd import ops
 
-    print("case: expert_map", flush=True)
-    c = make_case(T=200, H=256, I=256, E=8, k=2, BM=16, seed=33)
+    print(f"case: expert_map T={T}", flush=True)
+    c = make_case(T=T, H=256, I=256, E=8, k=2, BM=16, seed=33)
     local = [2, 5, 6]
     emap = np.full(c.E, -1, np.int32)
     emap[local] = np.arange(len(local), dtype=np.int32)
