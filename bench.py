@@ -33,9 +33,10 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 STAGES = ("quant", "align", "w13", "w2", "reduce")
 
 
-def stage_bytes(wl, ntpp: int, active: int) -> dict[str, float]:
+def stage_bytes(wl, ntpp: int, active: int, BM: int | None = None) -> dict[str, float]:
     """Algorithmic HBM bytes per launch of each stage (padding excluded)."""
-    T, H, I, E, k, BM = wl.T, wl.H, wl.I, wl.E, wl.top_k, wl.block_m
+    T, H, I, E, k = wl.T, wl.H, wl.I, wl.E, wl.top_k
+    BM = BM or wl.block_m
     S = T * k
     w13 = active * (2 * I * H + 4 * (2 * I // 128) * (H // 128))
     w2 = active * (H * I + 4 * (H // 128) * (I // 128))
@@ -123,6 +124,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="dsv3")
+    ap.add_argument("--block-m", type=int, default=0, help="override the workload's block_size_m")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline compute")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -137,11 +139,12 @@ def main() -> int:
 
     wl = workloads.CONFIGS[args.workload]
     data = workloads.generate(wl, "cuda")
-    runner = ops.FusedExpertsRunner(data.w13, data.w13_s, data.w2, data.w2_s, wl.T, wl.top_k, wl.block_m)
+    bm = args.block_m or wl.block_m
+    runner = ops.FusedExpertsRunner(data.w13, data.w13_s, data.w2, data.w2_s, wl.T, wl.top_k, bm)
     # Config 5 (n_chunks > 1): the headline time is the chunked pipeline over
     # n_streams HIP streams; per-stage times come from the single-pass runner.
     pipe = (ops.ChunkedExpertsRunner(data.w13, data.w13_s, data.w2, data.w2_s, wl.T, wl.top_k, wl.n_chunks,
-                                     wl.n_streams, wl.block_m) if wl.n_chunks > 1 else None)
+                                     wl.n_streams, bm) if wl.n_chunks > 1 else None)
 
     def step(ev=None):
         if ev is not None:
@@ -205,7 +208,7 @@ def main() -> int:
     ntpp = int(runner.align.ntpp.item())
     counts = torch.bincount(data.topk_ids.view(-1).long(), minlength=wl.E)
     active = int((counts > 0).sum().item())
-    sbytes = stage_bytes(wl, ntpp, active)
+    sbytes = stage_bytes(wl, ntpp, active, bm)
     flop_w13 = 4.0 * wl.S * wl.H * wl.I
     flop_w2 = 2.0 * wl.S * wl.H * wl.I
     gemm_ms = stage_ms["w13"] + stage_ms["w2"]
@@ -229,9 +232,10 @@ def main() -> int:
     else:
         roof = {"bound": "mfma", "achieved": w13_tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                 "frac": w13_tflops / PEAK_FP8_TFLOPS}
-    traffic, traffic_src = measured_traffic(wl.name, f"grouped_gemm_kernel<{wl.block_m},true>")
+    tm = ops.gemm_tile_rows(bm, wl.S, wl.E)
+    traffic, traffic_src = measured_traffic(wl.name, f"grouped_gemm_kernel<{tm},true>")
     roof.update({"traffic": traffic, "traffic_source": traffic_src,
-                 "kernel": f"grouped_gemm_kernel<{wl.block_m},true> (W13 + SiLU*up + 1x128 quant)",
+                 "kernel": f"grouped_gemm_kernel<{tm},true> (W13 + SiLU*up + 1x128 quant)",
                  "alg_bytes": sbytes["w13"], "alg_flop": flop_w13, "avg_us": stage_ms["w13"] * 1e3,
                  "mfma_frac": w13_tflops / PEAK_FP8_TFLOPS, "hbm_frac": w13_gbs / PEAK_HBM_GBS})
     result = {
@@ -249,7 +253,7 @@ def main() -> int:
         "data": "synthetic (N(0,1) activations, N(0,0.02) weights block-quantised 128x128, "
                 f"{wl.routing} top-{wl.top_k} routing)",
         "config": {"workload": wl.name, "T": wl.T, "H": wl.H, "I": wl.I, "E": wl.E,
-                   "top_k": wl.top_k, "block_size_m": wl.block_m, "routing": wl.routing,
+                   "top_k": wl.top_k, "block_size_m": bm, "gemm_tile_m": tm, "routing": wl.routing,
                    "n_chunks": wl.n_chunks, "n_streams": wl.n_streams,
                    "parallelism": "single GPU, all experts local"},
         "layer_us": ms_per_step * 1e3,

@@ -31,7 +31,7 @@ extern "C" {
 #define MOE_OK 0
 #define MOE_ERR_NULL_POINTER (-1)
 #define MOE_ERR_BAD_SHAPE (-2)      /* negative size, dimension not a multiple of 128, misaligned pointer */
-#define MOE_ERR_BAD_BLOCK_SIZE (-3) /* block_size_m not in {16, 32, 64, 128} */
+#define MOE_ERR_BAD_BLOCK_SIZE (-3) /* block_size_m not in {16, 32, 64, 128, 256} */
 #define MOE_ERR_CAPACITY (-4)       /* an output capacity is below what the shape needs */
 #define MOE_ERR_BAD_TOPK (-5)
 #define MOE_ERR_BAD_EXPERTS (-6)
@@ -85,7 +85,10 @@ int moe_align_block_size_mapped(const int32_t* topk_ids, int64_t S, int32_t E, i
  * C[s, n] = bf16( w[s]? * sum_kb dot(A[row,kb], B[e,n,kb]) * A_scale[row,kb] * B_scale[e,n/128,kb] )
  * for every placed slot s, row = a_by_pos ? (sorted position) : s / top_k.
  * topk_weights NULL = mul_routed_weight False.  A [rows,K], A_scale [rows,K/128],
- * B [E,N,K], B_scale [E,N/128,K/128], C [S,N] bf16.  N, K % 128 == 0. */
+ * B [E,N,K], B_scale [E,N/128,K/128], C [S,N] bf16.  N, K % 128 == 0.
+ * Every GEMM entry point without an explicit tile_m runs 256-row workgroup
+ * tiles (several consecutive align blocks of one expert) when S >= 160*E and
+ * block_size_m rows otherwise; the choice never changes the results. */
 int moe_grouped_gemm(const void* A, const float* A_scale, const void* B, const float* B_scale,
                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
                      const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
@@ -104,6 +107,18 @@ int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
                              const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
                              int64_t N, int64_t K, int32_t E, int32_t block_size_m,
                              int64_t max_padded, int32_t tile_order, void* C, void* stream);
+
+/* A5 / A8 with an explicit tile order and tile height: a workgroup computes
+ * tile_m rows = tile_m / block_size_m consecutive align blocks of one expert
+ * (the reference's kernel has one block per program, kernels.py:95-126; this
+ * is its BLOCK_SIZE_M choice made per launch without changing the align
+ * layout).  tile_m in {16, 32, 64, 128, 256}, a multiple of block_size_m;
+ * 0 = the automatic choice above.  Results are identical for every tile_m. */
+int moe_grouped_gemm_tiled(const void* A, const float* A_scale, const void* B, const float* B_scale,
+                           const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                           const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos,
+                           int64_t N, int64_t K, int32_t E, int32_t block_size_m, int64_t max_padded,
+                           int32_t tile_order, int32_t tile_m, void* C, void* stream);
 
 /* A5 / A8 on an N slice -- the reference's N-split wrapper
  * invoke_moe_kernel_n_split (overlap/kernels.py:219-310): computes
@@ -149,6 +164,13 @@ int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W1
                             const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
                             int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
                             int64_t max_padded, void* hq, float* hs, void* stream);
+
+/* The fused W13 with an explicit tile height (as moe_grouped_gemm_tiled). */
+int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const void* W13,
+                                  const float* W13_scale, const int32_t* sorted_ids,
+                                  const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                  int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
+                                  int64_t max_padded, int32_t tile_m, void* hq, float* hs, void* stream);
 
 /* A6 -- silu_and_mul.  Replaces torch.ops._C.silu_and_mul(out, in)
  * (overlap/overlap_forward.py:277-279): h[r,j] = bf16(silu(c[r,j]) * c[r,I+j]).

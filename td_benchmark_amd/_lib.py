@@ -43,6 +43,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                         _i64, _i32, _i32, _i64, _P, _P]),
     "moe_grouped_gemm_ordered": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32,
                                                 _i64, _i64, _i32, _i32, _i64, _i32, _P, _P]),
+    "moe_grouped_gemm_tiled": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32,
+                                              _i64, _i64, _i32, _i32, _i64, _i32, _i32, _P, _P]),
     "moe_grouped_gemm_n_split": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32, _i64,
                                                 _i64, _i64, _i64, _i32, _i32, _i64, _P, _P]),
     "moe_grouped_gemm_k_split": (ctypes.c_int, [_P, _P, _i64, _i64, _P, _P, _P, _P, _P, _P, _i64, _i32,
@@ -52,6 +54,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "moe_reduce_topk_add": (ctypes.c_int, [_P, _P, _i64, _i32, _i64, _P, _P]),
     "moe_gemm_w13_silu_quant": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
                                                _i64, _i32, _i32, _i64, _P, _P, _P]),
+    "moe_gemm_w13_silu_quant_tiled": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
+                                                     _i64, _i32, _i32, _i64, _i32, _P, _P, _P]),
     "moe_silu_and_mul": (ctypes.c_int, [_P, _i64, _i64, _P, _P]),
     "moe_reduce_topk": (ctypes.c_int, [_P, _i64, _i32, _i64, _P, _P]),
     "moe_debug_mfma_probe": (ctypes.c_int, [_P, _P, _P, _P]),

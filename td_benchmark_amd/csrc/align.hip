@@ -323,7 +323,7 @@ static int align_impl(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
                       void* workspace, void* stream) {
   if (S < 0) return kErrBadShape;
   if (E <= 0 || E > kAlignMaxExperts) return kErrBadExperts;
-  if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (!block_m_ok(BM)) return kErrBadBlockSize;
   if (!sorted_ids || !expert_ids || !ntpp || !workspace || (S > 0 && !topk_ids))
     return kErrNullPointer;
   if (max_padded < moe_align_max_padded(S, E, BM)) return kErrCapacity;

@@ -28,7 +28,7 @@ enum Status : int {
   kOk = 0,
   kErrNullPointer = -1,
   kErrBadShape = -2,        // a size is negative, or a dimension is not a multiple of 128
-  kErrBadBlockSize = -3,    // block_size_m not in {16, 32, 64, 128}
+  kErrBadBlockSize = -3,    // block_size_m not in {16, 32, 64, 128, 256}
   kErrCapacity = -4,        // an output buffer is smaller than the shape needs
   kErrBadTopK = -5,
   kErrBadExperts = -6,
@@ -39,6 +39,9 @@ static_assert(kErrNullPointer == MOE_ERR_NULL_POINTER && kErrBadShape == MOE_ERR
                   kErrBadTopK == MOE_ERR_BAD_TOPK && kErrBadExperts == MOE_ERR_BAD_EXPERTS &&
                   kErrLaunch == MOE_ERR_LAUNCH,
               "status codes must match the C header");
+
+// Block sizes the align and GEMM kernels are instantiated for.
+inline bool block_m_ok(int BM) { return BM == 16 || BM == 32 || BM == 64 || BM == 128 || BM == 256; }
 
 MOE_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 

@@ -62,14 +62,16 @@
 namespace moe {
 
 constexpr int kXcds = 8;
-constexpr int kStages = 3;
 constexpr int kMaxKB = 128;  // K <= 16384
 
 template <int BM>
 struct Tile {
   static constexpr int NW = BM >= 32 ? 8 : 4;     // waves per workgroup (2 per SIMD at 8)
   static constexpr int THREADS = 64 * NW;
-  static constexpr int WM = (NW == 8 || BM == 128) ? 2 : 1;  // waves along M
+  // waves along M: 4 x 2 waves of 64 x 128 at BM = 256 (fewer LDS bytes per MFMA)
+  static constexpr int WM = BM == 256 ? 4 : ((NW == 8 || BM == 128) ? 2 : 1);
+  // LDS ring depth: three 64 KiB stages of the 256-row tile exceed 160 KiB
+  static constexpr int KS = BM == 256 ? 2 : 3;
   static constexpr int WN = NW / WM;              // waves along N
   static constexpr int RS = BM / WM / 16;         // 16-row subtiles per wave
   static constexpr int CS = 8 / WN;               // 16-col subtiles per wave per group
@@ -91,8 +93,8 @@ struct Tile {
   }
   // loads of one stage per wave that may stay in flight while the older stage is consumed
   static constexpr int VM = vm_min();
-  static constexpr int OFF_SA = kStages * STAGE;
-  static constexpr int OFF_SB = OFF_SA + kStages * NS * 256;
+  static constexpr int OFF_SA = KS * STAGE;
+  static constexpr int OFF_SB = OFF_SA + KS * NS * 256;
   static constexpr int OFF_RED = OFF_SB + 2 * kMaxKB * 4;
   static constexpr int OFF_ROW = OFF_RED + WN * BM * 4;  // per-row slot id and routed weight
   static constexpr int LDS_BYTES = OFF_ROW + BM * 8;
@@ -117,8 +119,9 @@ struct GemmArgs {
   int64_t N;
   int64_t K;
   int64_t I;
-  int64_t max_blocks;
+  int64_t max_blocks;      // align blocks that fit in max_padded
   int64_t n_tiles;
+  int bma;                 // rows per align block (block_size_m); a tile spans BM / bma of them
   int top_k;
   int a_by_pos;
   int E;
@@ -205,7 +208,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
   // the same time on one XCD and fetch the weight tile from HBM once.
   const int ntpp = *g.ntpp;
-  const int64_t n_blocks = ntpp / BM;
+  const int64_t n_blocks = ntpp / g.bma;
   const int64_t total = n_blocks * g.n_tiles;
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   const int64_t pid = blockIdx.x;
@@ -257,16 +260,26 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
   const int64_t b0 = bq - back;
   const int64_t run = back + 1 + fwd;
-  // Inside a run, n-tiles go in groups of GG, block-major within a group:
-  // the GG workgroups that share an A block start together and reuse it from
-  // L2, and a weight tile is still read by all blocks of the run close in time.
+  // A tile spans ub consecutive align blocks of the run (one when BM equals
+  // the align block size); the run's `units` row tiles take its first
+  // units * n_tiles tile ids and the rest of its ids are idle.  Only the last
+  // block of a run holds padding, so a tile's valid rows are still a prefix.
+  const int64_t ub = BM / g.bma;
+  const int64_t units = (run + ub - 1) / ub;
   const int64_t in_run = t - b0 * g.n_tiles;
+  if (in_run >= units * g.n_tiles) return;
+  // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
+  // the GG workgroups that share an A tile start together and reuse it from
+  // L2, and a weight tile is still read by all row tiles of the run close in time.
   constexpr int64_t GG = FUSED ? 4 : 2;
-  const int64_t gj0 = in_run / (GG * run) * GG;
+  const int64_t gj0 = in_run / (GG * units) * GG;
   const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
-  const int64_t in_grp = in_run - gj0 * run;
-  const int64_t b = b0 + in_grp / gsz;
+  const int64_t in_grp = in_run - gj0 * units;
+  const int64_t b = b0 + in_grp / gsz * ub;    // first align block of the tile
   const int64_t j = gj0 + in_grp % gsz;
+  const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
+  // tile rows that belong to this run (the rest are not read or written)
+  const int rows_avail = (int)(((b0 + run - b) < ub ? (b0 + run - b) : ub) * g.bma);
   const int64_t K = g.K;
   const int KB = (int)(K / 128);
   const int64_t NBt = g.N / 128;
@@ -287,17 +300,17 @@ void grouped_gemm_kernel(GemmArgs g) {
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
     if (FUSED) {
-      for (int ci = tid; ci < BM * 8; ci += T::THREADS) {
+      for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
         const int row = ci >> 3, cc = ci & 7;
-        *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
+        *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
       }
-      for (int row = tid; row < BM; row += T::THREADS)
-        g.hs[(b * BM + row) * (g.I / 128) + j] = kScaleFloor;
+      for (int row = tid; row < rows_avail; row += T::THREADS)
+        g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
     } else {
       if (g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
-      for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
+      for (int ci = tid; ci < rows_avail * 32; ci += T::THREADS) {
         const int row = ci >> 5, cc = ci & 31;
-        const int64_t slot = g.sorted[b * BM + row];
+        const int64_t slot = g.sorted[pos0 + row];
         if (slot >= g.S) continue;
         const int grp = cc >> 4;
         if (grp == 1 && !g1_store) continue;
@@ -309,18 +322,18 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
 
   auto a_row_of = [&](int row) -> int64_t {
-    const int64_t pos = b * BM + row;
+    if (row >= rows_avail) return 0;
+    const int64_t pos = pos0 + row;
     if (g.a_by_pos) return pos;
     const int64_t slot = g.sorted[pos];
     return (slot < g.S) ? slot / g.top_k : 0;
   };
 
-  // Rows of this block that hold real slots (a prefix: padding follows them).
-  // The block's slot ids (and routed weights) once, for the epilogue; the
-  // valid rows of the block are a prefix (padding follows them).
+  // The tile's slot ids (and routed weights) once, for the epilogue; rows that
+  // hold real slots are a prefix (padding follows them).
   bool row_valid = false;
   if (tid < BM) {
-    const int32_t slot = g.sorted[b * BM + tid];
+    const int32_t slot = tid < rows_avail ? g.sorted[pos0 + tid] : (int32_t)g.S;
     row_valid = slot < g.S;
     smSlot[tid] = slot;
     if (!FUSED) smW[tid] = (g.topk_w && row_valid) ? g.topk_w[slot] : 1.0f;
@@ -359,13 +372,18 @@ void grouped_gemm_kernel(GemmArgs g) {
   const uint8_t* b_grp0 = g.B + (int64_t)e * g.b_es + g0 * 128 * g.ldb;
   const uint8_t* b_grp1 = g.B + (int64_t)e * g.b_es + g1 * 128 * g.ldb;
 
+  // With the two-stage ring every step waits for all of its loads (vmcnt 0), so
+  // the per-wave load count may vary: A rows of 16-row subtiles without a valid
+  // row (their MFMAs are skipped) are not fetched.  The three-stage ring's
+  // partial waits need the same count in every wave, so it fetches them all.
+  const int a_rows_needed = T::KS == 2 ? (nvalid + 15) / 16 * 16 : BM;
   auto issue_stage = [&](int kk, int stage) {
     uint8_t* dst = smem + stage * T::STAGE;
     const uint8_t* abase = g.A + kk * 128;
 #pragma unroll
     for (int i = 0; i < T::NA_W; ++i) {
       const int gi = wave + T::NW * i;
-      if (gi < T::NA) dma16(abase + a_off[i], dst + gi * 1024);
+      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase + a_off[i], dst + gi * 1024);
     }
     // B instruction gi = wave + NW*i covers tile rows 8*gi .. 8*gi+7 (group
     // i / (NB_W/2), row 8*wave + 8*NW*(i mod NB_W/2) + L/8 inside the group).
@@ -408,7 +426,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int sa_lane = row_base + 4 * kseg;
 
   issue_stage(0, 0);
-  if (KB > 1) issue_stage(1, 1);
+  if (T::KS == 3 && KB > 1) issue_stage(1, 1);
   wait_lgkm0();  // the weight-scale ds_writes above
 
   int ra = (nvalid - row_base + 15) / 16;
@@ -418,9 +436,11 @@ void grouped_gemm_kernel(GemmArgs g) {
     constexpr int RA = decltype(ra_c)::value;  // active 16-row subtiles of this wave
     int stage = 0;
     for (int kk = 0; kk < KB; ++kk) {
-      if (kk + 1 < KB) wait_vmcnt<T::VM>(); else wait_vmcnt<0>();
+      // Step kk's loads complete; with three stages step kk+1's may stay in flight.
+      if (T::KS == 3 && kk + 1 < KB) wait_vmcnt<T::VM>(); else wait_vmcnt<0>();
       block_barrier();
-      if (kk + 2 < KB) issue_stage(kk + 2, stage == 0 ? 2 : stage - 1);
+      // The buffer read at step kk-1 is free once every wave has passed the barrier.
+      if (kk + T::KS - 1 < KB) issue_stage(kk + T::KS - 1, stage == 0 ? T::KS - 1 : stage - 1);
       if constexpr (RA > 0) {
         const uint8_t* st = smem + stage * T::STAGE;
         const uint8_t* pa0 = st + a_lane0;
@@ -489,7 +509,7 @@ void grouped_gemm_kernel(GemmArgs g) {
             acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sab[ur][v], acc[ur][ug][uc][v]);
         }
       }
-      stage = (stage == 2) ? 0 : stage + 1;
+      stage = (stage == T::KS - 1) ? 0 : stage + 1;
     }
   };
   switch (ra) {
@@ -545,7 +565,7 @@ void grouped_gemm_kernel(GemmArgs g) {
         for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
         const float sc = group_scale(amax);
         const float inv = 1.0f / sc;
-        if (wn == 0 && fr == 0) g.hs[(b * BM + row) * hgroups + j] = sc;
+        if (wn == 0 && fr == 0 && row < rows_avail) g.hs[(pos0 + row) * hgroups + j] = sc;
 #pragma unroll
         for (int c = 0; c < T::CS; c += 2) {
           const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
@@ -556,9 +576,9 @@ void grouped_gemm_kernel(GemmArgs g) {
         }
       }
     __syncthreads();
-    for (int ci = tid; ci < BM * 8; ci += T::THREADS) {
+    for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
       const int row = ci >> 3, cc = ci & 7;
-      *reinterpret_cast<v4i*>(g.hq + (b * BM + row) * g.I + j * 128 + cc * 16) =
+      *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) =
           *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
     }
   } else {
@@ -623,17 +643,29 @@ static int launch_gemm(const GemmArgs& args, hipStream_t st) {
 }
 
 template <bool FUSED>
-static int dispatch_gemm(int BM, const GemmArgs& args, hipStream_t st) {
-  switch (BM) {
+static int dispatch_gemm(int TM, const GemmArgs& args, hipStream_t st) {
+  switch (TM) {
     case 16: return launch_gemm<16, FUSED>(args, st);
     case 32: return launch_gemm<32, FUSED>(args, st);
     case 64: return launch_gemm<64, FUSED>(args, st);
     case 128: return launch_gemm<128, FUSED>(args, st);
+    case 256: return launch_gemm<256, FUSED>(args, st);
     default: return kErrBadBlockSize;
   }
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Rows of a workgroup tile: tile_m / BM consecutive align blocks of one expert
+// share a tile.  0 picks 256 when the experts average at least 160 slots (the
+// weight tile is then fetched once per 256 rows instead of once per block) and
+// BM otherwise.  Returns -1 for a tile_m that is not a supported block size and
+// a multiple of BM.
+static int resolve_tile_m(int32_t tile_m, int32_t BM, int64_t S, int32_t E) {
+  if (tile_m == 0) return S >= 160 * (int64_t)E ? 256 : BM;
+  if (!block_m_ok(tile_m) || tile_m < BM || tile_m % BM != 0) return -1;
+  return tile_m;
+}
 
 // 32-bit lane offsets: every A row and every expert's B block must be
 // addressable with a uint32 offset from its base.
@@ -645,18 +677,20 @@ static bool offsets_fit(int64_t rows, int64_t N, int64_t K) {
 
 using namespace moe;
 
-extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
-                                        const float* B_scale, const int32_t* sorted_ids,
-                                        const int32_t* expert_ids, const int32_t* ntpp,
-                                        const float* topk_weights, int64_t S, int32_t top_k,
-                                        int32_t a_by_pos, int64_t N, int64_t K, int32_t E,
-                                        int32_t BM, int64_t max_padded, int32_t tile_order,
-                                        void* C, void* stream) {
+extern "C" int moe_grouped_gemm_tiled(const void* A, const float* A_scale, const void* B,
+                                      const float* B_scale, const int32_t* sorted_ids,
+                                      const int32_t* expert_ids, const int32_t* ntpp,
+                                      const float* topk_weights, int64_t S, int32_t top_k,
+                                      int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
+                                      int64_t max_padded, int32_t tile_order, int32_t tile_m,
+                                      void* C, void* stream) {
   if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
   if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
-  if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (!block_m_ok(BM)) return kErrBadBlockSize;
+  const int TM = resolve_tile_m(tile_m, BM, S, E);
+  if (TM < 0) return kErrBadBlockSize;
   if (tile_order < 0 || tile_order > 2) return kErrBadShape;
   if (max_padded == 0 || S == 0) return kOk;
   if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
@@ -680,12 +714,24 @@ extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, con
   g.I = 0;
   g.max_blocks = (max_padded + BM - 1) / BM;
   g.n_tiles = (N / 128 + 1) / 2;
+  g.bma = BM;
   g.top_k = top_k;
   g.a_by_pos = a_by_pos ? 1 : 0;
   g.E = E;
   g.tile_order = tile_order;
   dense_strides(g);
-  return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
+  return dispatch_gemm<false>(TM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
+                                        const float* B_scale, const int32_t* sorted_ids,
+                                        const int32_t* expert_ids, const int32_t* ntpp,
+                                        const float* topk_weights, int64_t S, int32_t top_k,
+                                        int32_t a_by_pos, int64_t N, int64_t K, int32_t E,
+                                        int32_t BM, int64_t max_padded, int32_t tile_order,
+                                        void* C, void* stream) {
+  return moe_grouped_gemm_tiled(A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S,
+                                top_k, a_by_pos, N, K, E, BM, max_padded, tile_order, 0, C, stream);
 }
 
 extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void* B,
@@ -701,15 +747,17 @@ extern "C" int moe_grouped_gemm(const void* A, const float* A_scale, const void*
 
 // Shared argument checks and setup of the plain-epilogue GEMM on (possibly
 // sliced) operands; the caller fills the strides and pre-offsets the bases.
-static int setup_plain(GemmArgs& g, const void* A, const float* A_scale, const void* B, const float* B_scale,
-                       const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
-                       const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos, int64_t N,
-                       int64_t K, int32_t E, int32_t BM, int64_t max_padded, void* C) {
+static int setup_plain(GemmArgs& g, int& TM, const void* A, const float* A_scale, const void* B,
+                       const float* B_scale, const int32_t* sorted_ids, const int32_t* expert_ids,
+                       const int32_t* ntpp, const float* topk_weights, int64_t S, int32_t top_k,
+                       int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM, int64_t max_padded,
+                       void* C) {
   if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
   if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
-  if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (!block_m_ok(BM)) return kErrBadBlockSize;
+  TM = resolve_tile_m(0, BM, S, E);
   if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
     return kErrNullPointer;
   g = GemmArgs{};
@@ -727,6 +775,7 @@ static int setup_plain(GemmArgs& g, const void* A, const float* A_scale, const v
   g.K = K;
   g.max_blocks = (max_padded + BM - 1) / BM;
   g.n_tiles = (N / 128 + 1) / 2;
+  g.bma = BM;
   g.top_k = top_k;
   g.a_by_pos = a_by_pos ? 1 : 0;
   g.E = E;
@@ -744,8 +793,9 @@ extern "C" int moe_grouped_gemm_n_split(const void* A, const float* A_scale, con
   if (full_N <= 0 || N_offset < 0 || N_chunk <= 0 || N_offset + N_chunk > full_N) return kErrBadShape;
   if (full_N % 128 != 0 || N_offset % 128 != 0) return kErrBadShape;
   GemmArgs g;
-  const int rc = setup_plain(g, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, top_k,
-                             a_by_pos, N_chunk, K, E, BM, max_padded, C);
+  int TM = 0;
+  const int rc = setup_plain(g, TM, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S,
+                             top_k, a_by_pos, N_chunk, K, E, BM, max_padded, C);
   if (rc != kOk || max_padded == 0 || S == 0) return rc;
   const int64_t KB = K / 128;
   // B[:, N_offset:N_offset+N_chunk, :], B_scale[:, N_offset/128:, :], C[:, N_offset:]
@@ -758,7 +808,7 @@ extern "C" int moe_grouped_gemm_n_split(const void* A, const float* A_scale, con
   if (!aligned16(g.A) || !aligned16(g.B) || !aligned16(g.C)) return kErrBadShape;
   const int64_t a_rows = a_by_pos ? max_padded : (S + top_k - 1) / top_k;
   if (!offsets_fit(a_rows, full_N, K)) return kErrBadShape;
-  return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
+  return dispatch_gemm<false>(TM, g, (hipStream_t)stream);
 }
 
 extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int64_t A_cols,
@@ -774,8 +824,9 @@ extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int
   if (full_K % 128 != 0 || K_offset % 128 != 0 || A_cols % 128 != 0 || A_K_offset % 128 != 0)
     return kErrBadShape;
   GemmArgs g;
-  const int rc = setup_plain(g, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, top_k,
-                             a_by_pos, N, K_chunk, E, BM, max_padded, C);
+  int TM = 0;
+  const int rc = setup_plain(g, TM, A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S,
+                             top_k, a_by_pos, N, K_chunk, E, BM, max_padded, C);
   if (rc != kOk || max_padded == 0 || S == 0) return rc;
   // A[:, A_K_offset:+K_chunk] of an [rows, A_cols] tensor (scales [rows, A_cols/128]),
   // B[:, :, K_offset:+K_chunk] of [E, N, full_K] (scales [E, N/128, full_K/128]).
@@ -793,20 +844,22 @@ extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int
   if (!aligned16(g.A) || !aligned16(g.B) || !aligned16(g.C)) return kErrBadShape;
   const int64_t a_rows = a_by_pos ? max_padded : (S + top_k - 1) / top_k;
   if (!offsets_fit(a_rows, N, full_K) || a_rows * A_cols >= ((int64_t)1 << 32)) return kErrBadShape;
-  return dispatch_gemm<false>(BM, g, (hipStream_t)stream);
+  return dispatch_gemm<false>(TM, g, (hipStream_t)stream);
 }
 
-extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,
-                                       const float* W13_scale, const int32_t* sorted_ids,
-                                       const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
-                                       int32_t top_k, int64_t H, int64_t I, int32_t E,
-                                       int32_t BM, int64_t max_padded, void* hq, float* hs,
-                                       void* stream) {
+extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const void* W13,
+                                             const float* W13_scale, const int32_t* sorted_ids,
+                                             const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                             int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM,
+                                             int64_t max_padded, int32_t tile_m, void* hq, float* hs,
+                                             void* stream) {
   if (S < 0 || H <= 0 || I <= 0 || max_padded < 0) return kErrBadShape;
   if (H % 128 != 0 || I % 128 != 0 || H > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
-  if (BM != 16 && BM != 32 && BM != 64 && BM != 128) return kErrBadBlockSize;
+  if (!block_m_ok(BM)) return kErrBadBlockSize;
+  const int TM = resolve_tile_m(tile_m, BM, S, E);
+  if (TM < 0) return kErrBadBlockSize;
   if (max_padded == 0 || S == 0) return kOk;
   if (!Aq || !A_scale || !W13 || !W13_scale || !sorted_ids || !expert_ids || !ntpp || !hq || !hs)
     return kErrNullPointer;
@@ -829,11 +882,22 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
   g.I = I;
   g.max_blocks = (max_padded + BM - 1) / BM;
   g.n_tiles = I / 128;
+  g.bma = BM;
   g.top_k = top_k;
   g.a_by_pos = 0;
   g.E = E;
   dense_strides(g);
-  return dispatch_gemm<true>(BM, g, (hipStream_t)stream);
+  return dispatch_gemm<true>(TM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,
+                                       const float* W13_scale, const int32_t* sorted_ids,
+                                       const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                       int32_t top_k, int64_t H, int64_t I, int32_t E,
+                                       int32_t BM, int64_t max_padded, void* hq, float* hs,
+                                       void* stream) {
+  return moe_gemm_w13_silu_quant_tiled(Aq, A_scale, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k,
+                                       H, I, E, BM, max_padded, 0, hq, hs, stream);
 }
 
 // Layout probe: one wave computes C[16][16] = A[16][128] . B[16][128]^T through

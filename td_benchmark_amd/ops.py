@@ -18,7 +18,7 @@ from ._lib import check, lib
 
 FP8 = torch.float8_e4m3fn
 BLOCK_SHAPE = [128, 128]
-SUPPORTED_BLOCK_M = (16, 32, 64, 128)
+SUPPORTED_BLOCK_M = (16, 32, 64, 128, 256)
 # workgroup -> tile orders of the grouped GEMM (include/moe_mi355x.h)
 TILE_ORDERS = {"expert_major": 0, "shuffled": 1, "half_phase": 2}
 
@@ -163,12 +163,13 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                               use_int8_w8a8: bool = False, use_int8_w8a16: bool = False,
                               use_int4_w4a16: bool = False, per_channel_quant: bool = False,
                               block_shape: list[int] | None = None, B_bias: Any = None,
-                              a_by_pos: bool = False, tile_order: int = 0) -> None:
+                              a_by_pos: bool = False, tile_order: int = 0, tile_m: int = 0) -> None:
     """The reference's grouped-GEMM call (overlap/kernels.py:288-310,
     schemes/shared_expert.py:102-123) on the FP8 w8a8 block-[128,128] form.
     C is [M, top_k, N] or [S, 1, N]; rows are written by slot.  ``tile_order``
-    selects the workgroup -> tile order (TILE_ORDERS); results do not depend
-    on it."""
+    selects the workgroup -> tile order (TILE_ORDERS) and ``tile_m`` the rows
+    of a workgroup tile (a multiple of BLOCK_SIZE_M up to 256; 0 = automatic);
+    results depend on neither."""
     if not use_fp8_w8a8 or use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or per_channel_quant:
         raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
     if B_zp is not None or B_bias is not None:
@@ -186,11 +187,11 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         if topk_weights is None:
             raise ValueError("mul_routed_weight requires topk_weights")
         w = topk_weights.contiguous().view(-1)
-    check(lib().moe_grouped_gemm_ordered(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale),
-                                         _ptr(sorted_token_ids), _ptr(expert_ids),
-                                         _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
-                                         1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(),
-                                         int(tile_order), _ptr(C), _stream()), "moe_grouped_gemm")
+    check(lib().moe_grouped_gemm_tiled(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale),
+                                       _ptr(sorted_token_ids), _ptr(expert_ids),
+                                       _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
+                                       1 if a_by_pos else 0, N, K, E, BM, sorted_token_ids.numel(),
+                                       int(tile_order), int(tile_m), _ptr(C), _stream()), "moe_grouped_gemm")
 
 
 def invoke_moe_kernel_n_split(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, A_scale: torch.Tensor,
@@ -276,9 +277,10 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
                         w13_scale: torch.Tensor, sorted_token_ids: torch.Tensor,
                         expert_ids: torch.Tensor, num_tokens_post_padded: torch.Tensor,
                         num_slots: int, top_k: int, block_size_m: int,
-                        hq: torch.Tensor | None = None, hs: torch.Tensor | None = None):
+                        hq: torch.Tensor | None = None, hs: torch.Tensor | None = None, tile_m: int = 0):
     """W13 GEMM + SiLU*up + 1x128 quant of h, outputs by sorted position:
-    (hq [max_padded, I] e4m3fn, hs [max_padded, I/128] fp32)."""
+    (hq [max_padded, I] e4m3fn, hs [max_padded, I/128] fp32).  ``tile_m`` as
+    for dispatch_fused_moe_kernel."""
     E, N2, H = w13.shape
     I = N2 // 2
     max_padded = sorted_token_ids.numel()
@@ -286,10 +288,11 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
         hq = torch.empty((max_padded, I), dtype=FP8, device=Aq.device)
     if hs is None:
         hs = torch.empty((max_padded, I // 128), dtype=torch.float32, device=Aq.device)
-    check(lib().moe_gemm_w13_silu_quant(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
-                                        _ptr(sorted_token_ids), _ptr(expert_ids),
-                                        _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
-                                        block_size_m, max_padded, _ptr(hq), _ptr(hs), _stream()),
+    check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
+                                              _ptr(sorted_token_ids), _ptr(expert_ids),
+                                              _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
+                                              block_size_m, max_padded, int(tile_m), _ptr(hq), _ptr(hs),
+                                              _stream()),
           "moe_gemm_w13_silu_quant")
     return hq, hs
 
@@ -347,6 +350,15 @@ def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int,
 # ---------------------------------------------------------------------------
 # A4 -- tile configuration
 # ---------------------------------------------------------------------------
+
+def gemm_tile_rows(block_size_m: int, num_slots: int, num_experts: int, tile_m: int = 0) -> int:
+    """Rows of the grouped GEMM's workgroup tile for this launch: ``tile_m`` if
+    given, else 256 when the experts average at least 160 slots and
+    ``block_size_m`` otherwise (the rule of the C entry points)."""
+    if tile_m:
+        return int(tile_m)
+    return 256 if num_slots >= 160 * num_experts else int(block_size_m)
+
 
 def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, int]:
     """Replacement for vLLM's try_get_optimal_moe_config (overlap_forward.py:
@@ -447,7 +459,8 @@ class FusedExpertsRunner:
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
                  shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None,
-                 global_num_experts: int | None = None, expert_map: torch.Tensor | None = None):
+                 global_num_experts: int | None = None, expert_map: torch.Tensor | None = None,
+                 tile_m: int = 0):
         for name, t in (("w13", w13), ("w2", w2)):
             _need(t, name, FP8)
         _need(w13_scale, "w13_scale", torch.float32)
@@ -460,6 +473,10 @@ class FusedExpertsRunner:
         self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
         if self.BM not in SUPPORTED_BLOCK_M:
             raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
+        # GEMM workgroup tile rows (0 = automatic; never changes the results)
+        self.tile_m = int(tile_m)
+        if self.tile_m and (self.tile_m not in SUPPORTED_BLOCK_M or self.tile_m % self.BM):
+            raise ValueError(f"tile_m must be a multiple of block_size_m in {SUPPORTED_BLOCK_M}")
         if shared is not None and (shared.H != H or shared.max_tokens < num_tokens):
             raise ValueError("shared expert does not match the layer's hidden size / token count")
         self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
@@ -502,19 +519,20 @@ class FusedExpertsRunner:
 
     def stage_w13(self) -> None:
         a = self.align
-        check(lib().moe_gemm_w13_silu_quant(_ptr(self.q1), _ptr(self.s1), _ptr(self.w13),
-                                            _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
-                                            _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
-                                            self.BM, a.max_padded, _ptr(self.hq), _ptr(self.hs),
-                                            _stream()), "moe_gemm_w13_silu_quant")
+        check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(self.q1), _ptr(self.s1), _ptr(self.w13),
+                                                  _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
+                                                  _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
+                                                  self.BM, a.max_padded, self.tile_m, _ptr(self.hq),
+                                                  _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
 
     def stage_w2(self, topk_weights: torch.Tensor) -> None:
         _need(topk_weights, "topk_weights", torch.float32)
         a = self.align
-        check(lib().moe_grouped_gemm(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
-                                     _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
-                                     _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
-                                     a.max_padded, _ptr(self.D), _stream()), "moe_grouped_gemm")
+        check(lib().moe_grouped_gemm_tiled(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
+                                           _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
+                                           _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
+                                           a.max_padded, 0, self.tile_m, _ptr(self.D), _stream()),
+              "moe_grouped_gemm")
 
     def stage_shared(self) -> None:
         """The shared expert on the layer's own FP8 input (no second quant)."""

@@ -196,6 +196,8 @@ GEMM_CASES = [
     (37, 384, 384, 16, 3, 32, "zipf"),       # ragged T, odd group counts
     (256, 1024, 768, 32, 4, 64, "softmax"),
     (128, 2048, 256, 64, 8, 16, "zipf"),
+    (600, 512, 384, 4, 2, 256, "softmax"),   # align blocks of 256 rows
+    (700, 256, 256, 4, 2, 64, "zipf"),       # S >= 160*E: 256-row tiles over 64-row blocks
 ]
 
 

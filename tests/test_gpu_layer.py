@@ -31,6 +31,7 @@ LAYER_CASES = [
     (128, 1024, 256, 64, 8, 32, "sigmoid"),     # 3: DSv3-like routing, reduced
     (32, 1024, 256, 64, 8, 16, "zipf"),         # 4: skewed decode, reduced
     (512, 256, 256, 32, 8, 64, "softmax"),      # 5: Qwen3-like, reduced
+    (1024, 512, 256, 8, 2, 128, "sigmoid"),     # S >= 160*E: 256-row tiles (pairs of blocks)
 ]
 
 

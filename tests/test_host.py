@@ -78,3 +78,12 @@ def test_ops_fail_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.lib()
+
+
+def test_gemm_tile_rows_rule():
+    from td_benchmark_amd import ops
+    assert ops.gemm_tile_rows(128, 65536, 256) == 256      # DSv3: 256 slots per expert
+    assert ops.gemm_tile_rows(16, 1024, 256) == 16         # decode
+    assert ops.gemm_tile_rows(64, 160 * 8, 8) == 256       # the threshold itself
+    assert ops.gemm_tile_rows(64, 160 * 8 - 1, 8) == 64
+    assert ops.gemm_tile_rows(64, 16, 8, tile_m=128) == 128
