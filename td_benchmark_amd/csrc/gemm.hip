@@ -235,28 +235,31 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
   if (t >= total) return;
   const int64_t bq = t / g.n_tiles;  // a block of the tile's run
-  const int e = g.eids[bq];
+  // The run of blocks with bq's expert: the expert ids of bq and of the 64
+  // blocks on either side are loaded together (one memory round trip for runs
+  // of up to 65 blocks), longer runs continue 64 blocks at a time.
   int64_t back = 0, fwd = 0;
+  int e;
   {
     const int ln = threadIdx.x & 63;
-    for (int64_t base = bq - 1;; base -= 64) {  // blocks before bq with the same expert
-      const int64_t idx = base - ln;
-      const uint64_t end = __ballot(!(idx >= 0 && g.eids[idx] == e));
-      if (end) {
-        back += __ffsll((unsigned long long)end) - 1;
-        break;
-      }
+    const int64_t ib = bq - 1 - ln, jf = bq + 1 + ln;
+    e = g.eids[bq];
+    const int xb = ib >= 0 ? g.eids[ib] : 0;
+    const int xf = jf < n_blocks ? g.eids[jf] : 0;
+    uint64_t end = __ballot(!(ib >= 0 && xb == e));  // blocks before bq with the same expert
+    for (int64_t base = bq - 1 - 64; !end; base -= 64) {
       back += 64;
+      const int64_t idx = base - ln;
+      end = __ballot(!(idx >= 0 && g.eids[idx] == e));
     }
-    for (int64_t base = bq + 1;; base += 64) {  // and after it
-      const int64_t idx = base + ln;
-      const uint64_t end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
-      if (end) {
-        fwd += __ffsll((unsigned long long)end) - 1;
-        break;
-      }
+    back += __ffsll((unsigned long long)end) - 1;
+    end = __ballot(!(jf < n_blocks && xf == e));      // and after it
+    for (int64_t base = bq + 1 + 64; !end; base += 64) {
       fwd += 64;
+      const int64_t idx = base + ln;
+      end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
     }
+    fwd += __ffsll((unsigned long long)end) - 1;
   }
   const int64_t b0 = bq - back;
   const int64_t run = back + 1 + fwd;
@@ -271,7 +274,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
   // the GG workgroups that share an A tile start together and reuse it from
   // L2, and a weight tile is still read by all row tiles of the run close in time.
-  constexpr int64_t GG = FUSED ? 4 : 2;
+  constexpr int64_t GG = FUSED ? 8 : 4;
   const int64_t gj0 = in_run / (GG * units) * GG;
   const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
   const int64_t in_grp = in_run - gj0 * units;
@@ -398,10 +401,14 @@ void grouped_gemm_kernel(GemmArgs g) {
            smem + T::OFF_SA + stage * T::NS * 256 + s_idx * 256);
   };
 
-  // Weight scales of both groups for every K block (read once, plain loads).
-  for (int i = tid; i < 2 * KB; i += T::THREADS) {
-    const int grp = i / KB, kk = i % KB;
-    smSB[grp * kMaxKB + kk] = g.Bs[(int64_t)e * g.bs_es + (grp ? g1 : g0) * g.bs_ld + kk];
+  // Weight scales of both groups for every K block (2*KB <= 256 <= THREADS:
+  // one per thread), loaded before the first stages are issued and stored to
+  // LDS after them, so their latency overlaps the first DMA.
+  static_assert(2 * kMaxKB <= T::THREADS, "one weight scale per thread");
+  float sb_val = 0.0f;
+  if (tid < 2 * KB) {
+    const int grp = tid / KB, kk = tid % KB;
+    sb_val = g.Bs[(int64_t)e * g.bs_es + (grp ? g1 : g0) * g.bs_ld + kk];
   }
 
   v4f acc[T::RS][2][T::CS];
@@ -427,7 +434,8 @@ void grouped_gemm_kernel(GemmArgs g) {
 
   issue_stage(0, 0);
   if (T::KS == 3 && KB > 1) issue_stage(1, 1);
-  wait_lgkm0();  // the weight-scale ds_writes above
+  if (tid < 2 * KB) smSB[(tid / KB) * kMaxKB + tid % KB] = sb_val;
+  wait_lgkm0();  // the weight-scale ds_writes
 
   int ra = (nvalid - row_base + 15) / 16;
   ra = ra < 0 ? 0 : (ra > T::RS ? T::RS : ra);
