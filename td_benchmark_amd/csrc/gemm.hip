@@ -63,6 +63,7 @@ namespace moe {
 
 constexpr int kXcds = 8;
 constexpr int kMaxKB = 128;  // K <= 16384
+constexpr int kTailRows = 64;  // row tiles with at most this many valid rows run the short body
 
 template <int BM>
 struct Tile {
@@ -182,147 +183,28 @@ MOE_DEVICE void dma4(const uint8_t* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 4, 0, 0);
 }
 
+// The tile's K loop and epilogue: rows [pos0, pos0 + rows_avail) of the sorted
+// order (a prefix of nvalid of them hold slots) times weight column groups g0,
+// g1 of expert e, with BM-row operand tiles.  A body with BM smaller than the
+// tile computes its first BM rows; the caller has checked that the rest are
+// padding.
 template <int BM, bool FUSED>
-__global__ __launch_bounds__(Tile<BM>::THREADS)
-__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4, Tile<BM>::NW / 4)))
-void grouped_gemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
+                                          int64_t g0, int64_t g1, bool g1_store, int nvalid) {
   using T = Tile<BM>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);
   float* smRed = reinterpret_cast<float*>(smem + T::OFF_RED);
   int32_t* smSlot = reinterpret_cast<int32_t*>(smem + T::OFF_ROW);
   float* smW = reinterpret_cast<float*>(smem + T::OFF_ROW + BM * 4);
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / T::WN;
   const int wn = wave % T::WN;
-
-  // ---- expert-aligned, XCD-aware tile mapping ----------------------------
-  // Tiles are ordered run-major: for each run of consecutive blocks with the
-  // same expert (blocks [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT),
-  // in groups of a few n-tiles (all n blocks of the run inside a group), so
-  // the blocks that read one weight tile are close together.  Workgroup ids
-  // are dealt round-robin to the XCDs; XCD x
-  // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
-  // the same time on one XCD and fetch the weight tile from HBM once.
-  const int ntpp = *g.ntpp;
-  const int64_t n_blocks = ntpp / g.bma;
-  const int64_t total = n_blocks * g.n_tiles;
-  const int64_t per_xcd = (total + kXcds - 1) / kXcds;
-  const int64_t pid = blockIdx.x;
-  int64_t t;
-  if (g.tile_order == 0) {
-    const int64_t local = pid / kXcds;
-    if (local >= per_xcd) return;
-    t = (pid % kXcds) * per_xcd + local;
-  } else if (g.tile_order == 1) {
-    // Shuffled arrival order: bit reversal within the next power of two,
-    // walked back into [0, total) (bit reversal is an involution, so a
-    // reversed index outside the range maps the id to itself: a bijection).
-    if (pid >= total) return;
-    int m = 0;
-    while (((int64_t)1 << m) < total) ++m;
-    const int64_t r = m ? (int64_t)(__builtin_bitreverse64((uint64_t)pid) >> (64 - m)) : 0;
-    t = r < total ? r : pid;
-  } else {
-    // Half-phase: the first and second halves of the expert-major order,
-    // interleaved tile by tile.
-    if (pid >= total) return;
-    const int64_t half = (total + 1) / 2;
-    t = (pid & 1) ? half + pid / 2 : pid / 2;
-  }
-  if (t >= total) return;
-  const int64_t bq = t / g.n_tiles;  // a block of the tile's run
-  // The run of blocks with bq's expert: the expert ids of bq and of the 64
-  // blocks on either side are loaded together (one memory round trip for runs
-  // of up to 65 blocks), longer runs continue 64 blocks at a time.
-  int64_t back = 0, fwd = 0;
-  int e;
-  {
-    const int ln = threadIdx.x & 63;
-    const int64_t ib = bq - 1 - ln, jf = bq + 1 + ln;
-    e = g.eids[bq];
-    const int xb = ib >= 0 ? g.eids[ib] : 0;
-    const int xf = jf < n_blocks ? g.eids[jf] : 0;
-    uint64_t end = __ballot(!(ib >= 0 && xb == e));  // blocks before bq with the same expert
-    for (int64_t base = bq - 1 - 64; !end; base -= 64) {
-      back += 64;
-      const int64_t idx = base - ln;
-      end = __ballot(!(idx >= 0 && g.eids[idx] == e));
-    }
-    back += __ffsll((unsigned long long)end) - 1;
-    end = __ballot(!(jf < n_blocks && xf == e));      // and after it
-    for (int64_t base = bq + 1 + 64; !end; base += 64) {
-      fwd += 64;
-      const int64_t idx = base + ln;
-      end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
-    }
-    fwd += __ffsll((unsigned long long)end) - 1;
-  }
-  const int64_t b0 = bq - back;
-  const int64_t run = back + 1 + fwd;
-  // A tile spans ub consecutive align blocks of the run (one when BM equals
-  // the align block size); the run's `units` row tiles take its first
-  // units * n_tiles tile ids and the rest of its ids are idle.  Only the last
-  // block of a run holds padding, so a tile's valid rows are still a prefix.
-  const int64_t ub = BM / g.bma;
-  const int64_t units = (run + ub - 1) / ub;
-  const int64_t in_run = t - b0 * g.n_tiles;
-  if (in_run >= units * g.n_tiles) return;
-  // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
-  // the GG workgroups that share an A tile start together and reuse it from
-  // L2, and a weight tile is still read by all row tiles of the run close in time.
-  constexpr int64_t GG = FUSED ? 8 : 4;
-  const int64_t gj0 = in_run / (GG * units) * GG;
-  const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
-  const int64_t in_grp = in_run - gj0 * units;
-  const int64_t b = b0 + in_grp / gsz * ub;    // first align block of the tile
-  const int64_t j = gj0 + in_grp % gsz;
-  const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
-  // tile rows that belong to this run (the rest are not read or written)
-  const int rows_avail = (int)(((b0 + run - b) < ub ? (b0 + run - b) : ub) * g.bma);
   const int64_t K = g.K;
   const int KB = (int)(K / 128);
-  const int64_t NBt = g.N / 128;
-  int64_t g0, g1;
-  bool g1_store = true;
-  if (FUSED) {
-    g0 = j;
-    g1 = g.I / 128 + j;
-  } else {
-    g0 = 2 * j;
-    g1 = 2 * j + 1;
-    if (g1 >= NBt) {
-      g1 = NBt - 1;
-      g1_store = false;
-    }
-  }
-
-  if (e < 0 || e >= g.E) {
-    // Expert not local: zero output rows (kernels.py:112-120).
-    if (FUSED) {
-      for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
-        const int row = ci >> 3, cc = ci & 7;
-        *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
-      }
-      for (int row = tid; row < rows_avail; row += T::THREADS)
-        g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
-    } else {
-      if (g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
-      for (int ci = tid; ci < rows_avail * 32; ci += T::THREADS) {
-        const int row = ci >> 5, cc = ci & 31;
-        const int64_t slot = g.sorted[pos0 + row];
-        if (slot >= g.S) continue;
-        const int grp = cc >> 4;
-        if (grp == 1 && !g1_store) continue;
-        const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
-        *reinterpret_cast<v4i*>(g.C + slot * g.ldc + n) = (v4i){0, 0, 0, 0};
-      }
-    }
-    return;
-  }
+  if (rows_avail > BM) rows_avail = BM;
 
   auto a_row_of = [&](int row) -> int64_t {
     if (row >= rows_avail) return 0;
@@ -334,14 +216,13 @@ void grouped_gemm_kernel(GemmArgs g) {
 
   // The tile's slot ids (and routed weights) once, for the epilogue; rows that
   // hold real slots are a prefix (padding follows them).
-  bool row_valid = false;
+  // The tile's slot ids (and routed weights) for the epilogue; the barriers
+  // of the K loop order these writes before their use.
   if (tid < BM) {
     const int32_t slot = tid < rows_avail ? g.sorted[pos0 + tid] : (int32_t)g.S;
-    row_valid = slot < g.S;
     smSlot[tid] = slot;
-    if (!FUSED) smW[tid] = (g.topk_w && row_valid) ? g.topk_w[slot] : 1.0f;
+    if (!FUSED) smW[tid] = (g.topk_w && slot < g.S) ? g.topk_w[slot] : 1.0f;
   }
-  const int nvalid = __syncthreads_count(row_valid);
 
   // ---- per-lane DMA offsets (32-bit, relative to uniform bases) ----------
   // A instruction gi = wave + 4*i covers tile rows 8*gi .. 8*gi+7; lane L fills
@@ -630,6 +511,165 @@ void grouped_gemm_kernel(GemmArgs g) {
       *dst = val;
     }
   }
+}
+
+template <int BM, bool FUSED>
+__global__ __launch_bounds__(Tile<BM>::THREADS)
+__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4, Tile<BM>::NW / 4)))
+void grouped_gemm_kernel(GemmArgs g) {
+  using T = Tile<BM>;
+  static_assert(BM <= kTailRows || Tile<kTailRows>::LDS_BYTES <= T::LDS_BYTES,
+                "the short body must fit in the launch's LDS");
+  static_assert(BM <= kTailRows || Tile<kTailRows>::THREADS == T::THREADS, "same workgroup size");
+  const int tid = threadIdx.x;
+
+  // ---- expert-aligned, XCD-aware tile mapping ----------------------------
+  // Tiles are ordered run-major: for each run of consecutive blocks with the
+  // same expert (blocks [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT),
+  // in groups of a few n-tiles (all n blocks of the run inside a group), so
+  // the blocks that read one weight tile are close together.  Workgroup ids
+  // are dealt round-robin to the XCDs; XCD x
+  // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
+  // the same time on one XCD and fetch the weight tile from HBM once.
+  const int ntpp = *g.ntpp;
+  const int64_t n_blocks = ntpp / g.bma;
+  const int64_t total = n_blocks * g.n_tiles;
+  const int64_t per_xcd = (total + kXcds - 1) / kXcds;
+  const int64_t pid = blockIdx.x;
+  int64_t t;
+  if (g.tile_order == 0) {
+    const int64_t local = pid / kXcds;
+    if (local >= per_xcd) return;
+    t = (pid % kXcds) * per_xcd + local;
+  } else if (g.tile_order == 1) {
+    // Shuffled arrival order: bit reversal within the next power of two,
+    // walked back into [0, total) (bit reversal is an involution, so a
+    // reversed index outside the range maps the id to itself: a bijection).
+    if (pid >= total) return;
+    int m = 0;
+    while (((int64_t)1 << m) < total) ++m;
+    const int64_t r = m ? (int64_t)(__builtin_bitreverse64((uint64_t)pid) >> (64 - m)) : 0;
+    t = r < total ? r : pid;
+  } else {
+    // Half-phase: the first and second halves of the expert-major order,
+    // interleaved tile by tile.
+    if (pid >= total) return;
+    const int64_t half = (total + 1) / 2;
+    t = (pid & 1) ? half + pid / 2 : pid / 2;
+  }
+  if (t >= total) return;
+  const int64_t bq = t / g.n_tiles;  // a block of the tile's run
+  // The run of blocks with bq's expert: the expert ids of bq and of the 64
+  // blocks on either side are loaded together (one memory round trip for runs
+  // of up to 65 blocks), longer runs continue 64 blocks at a time.
+  int64_t back = 0, fwd = 0;
+  int e;
+  {
+    const int ln = threadIdx.x & 63;
+    const int64_t ib = bq - 1 - ln, jf = bq + 1 + ln;
+    e = g.eids[bq];
+    const int xb = ib >= 0 ? g.eids[ib] : 0;
+    const int xf = jf < n_blocks ? g.eids[jf] : 0;
+    uint64_t end = __ballot(!(ib >= 0 && xb == e));  // blocks before bq with the same expert
+    for (int64_t base = bq - 1 - 64; !end; base -= 64) {
+      back += 64;
+      const int64_t idx = base - ln;
+      end = __ballot(!(idx >= 0 && g.eids[idx] == e));
+    }
+    back += __ffsll((unsigned long long)end) - 1;
+    end = __ballot(!(jf < n_blocks && xf == e));      // and after it
+    for (int64_t base = bq + 1 + 64; !end; base += 64) {
+      fwd += 64;
+      const int64_t idx = base + ln;
+      end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
+    }
+    fwd += __ffsll((unsigned long long)end) - 1;
+  }
+  const int64_t b0 = bq - back;
+  const int64_t run = back + 1 + fwd;
+  // A tile spans ub consecutive align blocks of the run (one when BM equals
+  // the align block size); the run's `units` row tiles take its first
+  // units * n_tiles tile ids and the rest of its ids are idle.  Only the last
+  // block of a run holds padding, so a tile's valid rows are still a prefix.
+  const int64_t ub = BM / g.bma;
+  const int64_t units = (run + ub - 1) / ub;
+  const int64_t in_run = t - b0 * g.n_tiles;
+  if (in_run >= units * g.n_tiles) return;
+  // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
+  // the GG workgroups that share an A tile start together and reuse it from
+  // L2, and a weight tile is still read by all row tiles of the run close in time.
+  constexpr int64_t GG = FUSED ? 8 : 4;
+  const int64_t gj0 = in_run / (GG * units) * GG;
+  const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
+  const int64_t in_grp = in_run - gj0 * units;
+  const int64_t b = b0 + in_grp / gsz * ub;    // first align block of the tile
+  const int64_t j = gj0 + in_grp % gsz;
+  const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
+  // tile rows that belong to this run (the rest are not read or written)
+  const int rows_avail = (int)(((b0 + run - b) < ub ? (b0 + run - b) : ub) * g.bma);
+  const int64_t NBt = g.N / 128;
+  int64_t g0, g1;
+  bool g1_store = true;
+  if (FUSED) {
+    g0 = j;
+    g1 = g.I / 128 + j;
+  } else {
+    g0 = 2 * j;
+    g1 = 2 * j + 1;
+    if (g1 >= NBt) {
+      g1 = NBt - 1;
+      g1_store = false;
+    }
+  }
+
+  if (e < 0 || e >= g.E) {
+    // Expert not local: zero output rows (kernels.py:112-120).
+    if (FUSED) {
+      for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
+        const int row = ci >> 3, cc = ci & 7;
+        *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
+      }
+      for (int row = tid; row < rows_avail; row += T::THREADS)
+        g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
+    } else {
+      if (g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
+      for (int ci = tid; ci < rows_avail * 32; ci += T::THREADS) {
+        const int row = ci >> 5, cc = ci & 31;
+        const int64_t slot = g.sorted[pos0 + row];
+        if (slot >= g.S) continue;
+        const int grp = cc >> 4;
+        if (grp == 1 && !g1_store) continue;
+        const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
+        *reinterpret_cast<v4i*>(g.C + slot * g.ldc + n) = (v4i){0, 0, 0, 0};
+      }
+    }
+    return;
+  }
+
+  // Rows of the tile that hold real slots (a prefix: padding follows them).
+  bool row_valid = false;
+  if (tid < BM && tid < rows_avail) row_valid = g.sorted[pos0 + tid] < g.S;
+  const int nvalid = __syncthreads_count(row_valid);
+  if constexpr (BM > kTailRows) {
+    // A tile with few valid rows (an expert's last rows) is bound by streaming
+    // its weight tile: it runs with kTailRows-row operand tiles, whose small
+    // stages give a three-deep LDS ring, and a kTailRows-row epilogue.  Rows
+    // past kTailRows are padding; the fused outputs of those positions are the
+    // zero codes and floor scales an all-zero row quantises to.
+    if (nvalid <= kTailRows) {
+      gemm_tile<kTailRows, FUSED>(g, j, pos0, rows_avail, e, g0, g1, g1_store, nvalid);
+      if (FUSED) {
+        for (int ci = kTailRows * 8 + tid; ci < rows_avail * 8; ci += T::THREADS) {
+          const int row = ci >> 3, cc = ci & 7;
+          *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
+        }
+        for (int row = kTailRows + tid; row < rows_avail; row += T::THREADS)
+          g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
+      }
+      return;
+    }
+  }
+  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, g0, g1, g1_store, nvalid);
 }
 
 template <int BM, bool FUSED>
