@@ -121,7 +121,7 @@ struct GemmArgs {
   int64_t K;
   int64_t I;
   int64_t max_blocks;      // align blocks that fit in max_padded
-  int64_t n_tiles;
+  int64_t n_tiles;         // 256-column n-tiles
   int bma;                 // rows per align block (block_size_m); a tile spans BM / bma of them
   int top_k;
   int a_by_pos;
@@ -183,23 +183,40 @@ MOE_DEVICE void dma4(const uint8_t* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 4, 0, 0);
 }
 
-// The tile's K loop and epilogue: rows [pos0, pos0 + rows_avail) of the sorted
-// order (a prefix of nvalid of them hold slots) times weight column groups g0,
-// g1 of expert e, with BM-row operand tiles.  A body with BM smaller than the
-// tile computes its first BM rows; the caller has checked that the rest are
-// padding.
+// Column scale groups of n-tile j: W13 gate group j and up group I/128 + j; the
+// plain GEMM groups 2j and 2j+1 (the second absent past N).
+template <bool FUSED>
+MOE_DEVICE void groups_of(const GemmArgs& g, int64_t j, int64_t& g0, int64_t& g1, bool& g1_store) {
+  if (FUSED) {
+    g0 = j;
+    g1 = g.I / 128 + j;
+    g1_store = true;
+  } else {
+    const int64_t nbt = g.N / 128;
+    g0 = 2 * j;
+    g1 = 2 * j + 1;
+    g1_store = g1 < nbt;
+    if (!g1_store) g1 = nbt - 1;
+  }
+}
+
+// The K loop and epilogue of one tile: n-tile j of rows [pos0, pos0 +
+// rows_avail) of the sorted order (a prefix of nvalid of them hold slots) of
+// expert e, with BM-row operand tiles.  A body with BM smaller than the tile
+// computes its first BM rows; the caller has checked that the rest are padding.
 template <int BM, bool FUSED>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
-                                          int64_t g0, int64_t g1, bool g1_store, int nvalid) {
+                                          int nvalid) {
   using T = Tile<BM>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);
+  float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);  // [2 groups][kMaxKB]
   float* smRed = reinterpret_cast<float*>(smem + T::OFF_RED);
   int32_t* smSlot = reinterpret_cast<int32_t*>(smem + T::OFF_ROW);
   float* smW = reinterpret_cast<float*>(smem + T::OFF_ROW + BM * 4);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform values live in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / T::WN;
   const int wn = wave % T::WN;
   const int64_t K = g.K;
@@ -214,9 +231,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     return (slot < g.S) ? slot / g.top_k : 0;
   };
 
-  // The tile's slot ids (and routed weights) once, for the epilogue; rows that
-  // hold real slots are a prefix (padding follows them).
-  // The tile's slot ids (and routed weights) for the epilogue; the barriers
+  // The tile's slot ids (and routed weights) for the epilogues; the barriers
   // of the K loop order these writes before their use.
   if (tid < BM) {
     const int32_t slot = tid < rows_avail ? g.sorted[pos0 + tid] : (int32_t)g.S;
@@ -225,7 +240,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   }
 
   // ---- per-lane DMA offsets (32-bit, relative to uniform bases) ----------
-  // A instruction gi = wave + 4*i covers tile rows 8*gi .. 8*gi+7; lane L fills
+  // A instruction gi = wave + NW*i covers tile rows 8*gi .. 8*gi+7; lane L fills
   // LDS slot L&7 of row R = 8*gi + L/8 with logical chunk slot_of(L&7, R).
   uint32_t a_off[T::NA_W > 0 ? T::NA_W : 1];
 #pragma unroll
@@ -235,11 +250,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     const int cc = slot_of(lane & 7, row);
     a_off[i] = (uint32_t)(a_row_of(row) * g.lda) + (uint32_t)(cc * 16);
   }
-  // B instruction gi = wave + 4*i (i < 8) covers B-tile rows 8*gi .. 8*gi+7;
-  // tile rows 0..127 are scale group g0, rows 128..255 group g1.  The lane's
-  // row inside its group is 8*wave + 32*(i%4) + L/8, and its rotation does not
-  // depend on i (32*i leaves row mod 16 and bit 3 unchanged), so one lane
-  // offset serves all eight instructions; the rest is a uniform base.
+  // B instruction gi = wave + NW*i covers B-tile rows 8*gi .. 8*gi+7; tile rows
+  // 0..127 are scale group g0, rows 128..255 group g1.  The lane's row inside its
+  // group is 8*wave + 8*NW*(i mod NB_W/2) + L/8, and its rotation does not
+  // depend on i (8*NW*i leaves row mod 16 and bit 3 unchanged), so one lane
+  // offset serves every instruction; the rest is a uniform base.
   uint32_t b_off;
   {
     const int r0 = 8 * wave + (lane >> 3);
@@ -253,33 +268,47 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     const int row = 64 * s_idx + lane;
     sa_off = (uint32_t)(a_row_of(row < BM ? row : 0) * g.as_ld) * 4u;
   }
-  const uint8_t* b_grp0 = g.B + (int64_t)e * g.b_es + g0 * 128 * g.ldb;
-  const uint8_t* b_grp1 = g.B + (int64_t)e * g.b_es + g1 * 128 * g.ldb;
+  int64_t g0, g1;
+  bool g1_store;
+  groups_of<FUSED>(g, j, g0, g1, g1_store);
+  const uint8_t* b_expert = g.B + (int64_t)e * g.b_es;
+  const float* bs_expert = g.Bs + (int64_t)e * g.bs_es;
+  const uint8_t* bg0 = b_expert + g0 * 128 * g.ldb;  // the tile's two weight groups
+  const uint8_t* bg1 = b_expert + g1 * 128 * g.ldb;
 
   // With the two-stage ring every step waits for all of its loads (vmcnt 0), so
   // the per-wave load count may vary: A rows of 16-row subtiles without a valid
   // row (their MFMAs are skipped) are not fetched.  The three-stage ring's
   // partial waits need the same count in every wave, so it fetches them all.
   const int a_rows_needed = T::KS == 2 ? (nvalid + 15) / 16 * 16 : BM;
-  auto issue_stage = [&](int kk, int stage) {
+  // Stage `stage` <- K block kk of the A rows and of weight groups at bg0, bg1.
+  // The 32-bit lane offsets pass through an empty asm at every issue, so the
+  // 64-bit per-lane addresses are formed where they are used instead of being
+  // hoisted and kept live (which exhausts the registers of the 256-row tile).
+  auto issue_stage = [&](int kk, int stage, const uint8_t* bg0, const uint8_t* bg1) {
     uint8_t* dst = smem + stage * T::STAGE;
     const uint8_t* abase = g.A + kk * 128;
 #pragma unroll
     for (int i = 0; i < T::NA_W; ++i) {
       const int gi = wave + T::NW * i;
-      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase + a_off[i], dst + gi * 1024);
+      uint32_t off = a_off[i];
+      asm volatile("" : "+v"(off));
+      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase + off, dst + gi * 1024);
     }
-    // B instruction gi = wave + NW*i covers tile rows 8*gi .. 8*gi+7 (group
-    // i / (NB_W/2), row 8*wave + 8*NW*(i mod NB_W/2) + L/8 inside the group).
+    uint32_t boff = b_off;
+    asm volatile("" : "+v"(boff));
     constexpr int HALF = T::NB_W / 2;
 #pragma unroll
     for (int i = 0; i < T::NB_W; ++i) {
-      const uint8_t* bbase = (i < HALF ? b_grp0 : b_grp1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
-      dma16(bbase + b_off, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+      const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
+      dma16(bbase + boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
     }
-    if (s_idx < T::NS)
-      dma4(reinterpret_cast<const uint8_t*>(g.As + kk) + sa_off,
+    if (s_idx < T::NS) {
+      uint32_t soff = sa_off;
+      asm volatile("" : "+v"(soff));
+      dma4(reinterpret_cast<const uint8_t*>(g.As + kk) + soff,
            smem + T::OFF_SA + stage * T::NS * 256 + s_idx * 256);
+    }
   };
 
   // Weight scales of both groups for every K block (2*KB <= 256 <= THREADS:
@@ -287,18 +316,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   // LDS after them, so their latency overlaps the first DMA.
   static_assert(2 * kMaxKB <= T::THREADS, "one weight scale per thread");
   float sb_val = 0.0f;
-  if (tid < 2 * KB) {
-    const int grp = tid / KB, kk = tid % KB;
-    sb_val = g.Bs[(int64_t)e * g.bs_es + (grp ? g1 : g0) * g.bs_ld + kk];
-  }
-
-  v4f acc[T::RS][2][T::CS];
-#pragma unroll
-  for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-    for (int gg = 0; gg < 2; ++gg)
-#pragma unroll
-      for (int c = 0; c < T::CS; ++c) acc[r][gg][c] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+  if (tid < 2 * KB) sb_val = bs_expert[(tid < KB ? g0 : g1) * g.bs_ld + tid % KB];
 
   const int row_base = wm * T::RS * 16;
   const int col_base = wn * T::CS * 16;
@@ -313,14 +331,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   const float* smSA = reinterpret_cast<const float*>(smem + T::OFF_SA);
   const int sa_lane = row_base + 4 * kseg;
 
-  issue_stage(0, 0);
-  if (T::KS == 3 && KB > 1) issue_stage(1, 1);
+  issue_stage(0, 0, bg0, bg1);
+  if (T::KS == 3 && KB > 1) issue_stage(1, 1, bg0, bg1);
   if (tid < 2 * KB) smSB[(tid / KB) * kMaxKB + tid % KB] = sb_val;
   wait_lgkm0();  // the weight-scale ds_writes
 
   int ra = (nvalid - row_base + 15) / 16;
   ra = ra < 0 ? 0 : (ra > T::RS ? T::RS : ra);
 
+  v4f acc[T::RS][2][T::CS];
+#pragma unroll
+  for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+      for (int c = 0; c < T::CS; ++c) acc[r][gg][c] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+
+  int stage_last = 0;
   auto kloop = [&](auto ra_c) {
     constexpr int RA = decltype(ra_c)::value;  // active 16-row subtiles of this wave
     int stage = 0;
@@ -329,7 +356,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
       if (T::KS == 3 && kk + 1 < KB) wait_vmcnt<T::VM>(); else wait_vmcnt<0>();
       block_barrier();
       // The buffer read at step kk-1 is free once every wave has passed the barrier.
-      if (kk + T::KS - 1 < KB) issue_stage(kk + T::KS - 1, stage == 0 ? T::KS - 1 : stage - 1);
+      if (kk + T::KS - 1 < KB) issue_stage(kk + T::KS - 1, stage == 0 ? T::KS - 1 : stage - 1, bg0, bg1);
       if constexpr (RA > 0) {
         const uint8_t* st = smem + stage * T::STAGE;
         const uint8_t* pa0 = st + a_lane0;
@@ -398,6 +425,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
             acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sab[ur][v], acc[ur][ug][uc][v]);
         }
       }
+      stage_last = stage;
       stage = (stage == T::KS - 1) ? 0 : stage + 1;
     }
   };
@@ -408,7 +436,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     case 3: if constexpr (T::RS >= 3) kloop(std::integral_constant<int, (T::RS >= 3 ? 3 : 0)>{}); break;
     default: if constexpr (T::RS >= 4) kloop(std::integral_constant<int, (T::RS >= 4 ? 4 : 0)>{}); break;
   }
-  block_barrier();  // every wave is done with the ring; reuse it for staging
+  block_barrier();  // every wave is done with the last step's buffer; stage the output there
 
   // ---- epilogues ----------------------------------------------------------
   // Output element (r, gg, c, v) of this lane: row = row_base + r*16 + 4*kseg + v,
@@ -442,7 +470,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         if (fr == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
       }
     __syncthreads();
-    uint8_t* stage_out = smem;  // [BM][128] fp8 codes
+    uint8_t* stage_out = smem + stage_last * T::STAGE;  // [BM][128] fp8 codes
     const int64_t hgroups = g.I / 128;
 #pragma unroll
     for (int r = 0; r < T::RS; ++r)
@@ -471,46 +499,50 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
           *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
     }
   } else {
-    uint16_t* stage_out = reinterpret_cast<uint16_t*>(smem);  // [BM][256] bf16
+    // One 128-column group per pass, staged as [BM][128] bf16 in the last
+    // step's buffer (BM*256 B fits in a stage for every BM).
+    static_assert(BM * 256 <= T::STAGE, "one group's bf16 output must fit in a stage");
+    uint16_t* stage_out = reinterpret_cast<uint16_t*>(smem + stage_last * T::STAGE);
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r)
+    for (int gg = 0; gg < 2; ++gg) {
+      if (gg == 1 && !g1_store) break;
+      if (gg == 1) __syncthreads();  // the first pass's stores have read the staging
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = row_base + r * 16 + 4 * kseg + v;
-        const float w = smW[row];
+      for (int r = 0; r < T::RS; ++r)
 #pragma unroll
-        for (int gg = 0; gg < 2; ++gg)
+        for (int v = 0; v < 4; ++v) {
+          const int row = row_base + r * 16 + 4 * kseg + v;
+          const float w = smW[row];
 #pragma unroll
           for (int c = 0; c < T::CS; ++c) {
             float val = acc[r][gg][c][v];
             if (g.topk_w) val = val * w;
-            stage_out[row * 256 + gg * 128 + col_base + c * 16 + fr] =
-                (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
+            stage_out[row * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
           }
-      }
-    __syncthreads();
-    for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
-      const int row = ci >> 5, cc = ci & 31;
-      const int64_t slot = smSlot[row];
-      if (slot >= g.S) continue;
-      const int grp = cc >> 4;
-      if (grp == 1 && !g1_store) continue;
-      const int64_t n = (grp ? g1 : g0) * 128 + (cc & 15) * 8;
-      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
-      v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
-      if (g.accumulate) {
-        // K-split accumulation: the bf16 partial is added to the bf16 C of the
-        // earlier chunks and rounded again.
-        const v4i old = *dst;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
-          val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
         }
+      __syncthreads();
+      const int64_t n0 = (gg ? g1 : g0) * 128;
+      for (int ci = tid; ci < BM * 16; ci += T::THREADS) {
+        const int row = ci >> 4, cc = ci & 15;
+        const int64_t slot = smSlot[row];
+        if (slot >= g.S) continue;
+        v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 8);
+        v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n0 + cc * 8);
+        if (g.accumulate) {
+          // K-split accumulation: the bf16 partial is added to the bf16 C of the
+          // earlier chunks and rounded again.
+          const v4i old = *dst;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
+            val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
+          }
+        }
+        *dst = val;
       }
-      *dst = val;
     }
   }
+
 }
 
 template <int BM, bool FUSED>
@@ -524,13 +556,14 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x;
 
   // ---- expert-aligned, XCD-aware tile mapping ----------------------------
-  // Tiles are ordered run-major: for each run of consecutive blocks with the
-  // same expert (blocks [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT),
-  // in groups of a few n-tiles (all n blocks of the run inside a group), so
-  // the blocks that read one weight tile are close together.  Workgroup ids
-  // are dealt round-robin to the XCDs; XCD x
-  // takes the contiguous range t in [x*C, (x+1)*C), so those blocks run at
-  // the same time on one XCD and fetch the weight tile from HBM once.
+  // A workgroup computes one row tile by one n-tile.  Tiles are ordered
+  // run-major: for each run of consecutive blocks with the same expert (blocks
+  // [b0, b0+n)), its tiles are t in [b0*NT, (b0+n)*NT), in groups of a few
+  // n-tiles (all row tiles of the run inside a group), so the row tiles that
+  // read one weight tile are close together.  Workgroup ids are dealt
+  // round-robin to the XCDs; XCD x takes the contiguous range t in
+  // [x*C, (x+1)*C), so those row tiles run at the same time on one XCD and
+  // fetch the weight tile from HBM once.
   const int ntpp = *g.ntpp;
   const int64_t n_blocks = ntpp / g.bma;
   const int64_t total = n_blocks * g.n_tiles;
@@ -587,9 +620,9 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
   const int64_t b0 = bq - back;
   const int64_t run = back + 1 + fwd;
-  // A tile spans ub consecutive align blocks of the run (one when BM equals
+  // A row tile spans ub consecutive align blocks of the run (one when BM equals
   // the align block size); the run's `units` row tiles take its first
-  // units * n_tiles tile ids and the rest of its ids are idle.  Only the last
+  // units * NT tile ids and the rest of its ids are idle.  Only the last
   // block of a run holds padding, so a tile's valid rows are still a prefix.
   const int64_t ub = BM / g.bma;
   const int64_t units = (run + ub - 1) / ub;
@@ -607,23 +640,13 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
   // tile rows that belong to this run (the rest are not read or written)
   const int rows_avail = (int)(((b0 + run - b) < ub ? (b0 + run - b) : ub) * g.bma);
-  const int64_t NBt = g.N / 128;
-  int64_t g0, g1;
-  bool g1_store = true;
-  if (FUSED) {
-    g0 = j;
-    g1 = g.I / 128 + j;
-  } else {
-    g0 = 2 * j;
-    g1 = 2 * j + 1;
-    if (g1 >= NBt) {
-      g1 = NBt - 1;
-      g1_store = false;
-    }
-  }
 
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
+    if (!FUSED && g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
+    int64_t g0, g1;
+    bool g1_store;
+    groups_of<FUSED>(g, j, g0, g1, g1_store);
     if (FUSED) {
       for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
         const int row = ci >> 3, cc = ci & 7;
@@ -632,7 +655,6 @@ void grouped_gemm_kernel(GemmArgs g) {
       for (int row = tid; row < rows_avail; row += T::THREADS)
         g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
     } else {
-      if (g.accumulate) return;  // later K chunks leave C as it is (kernels.py:112-120)
       for (int ci = tid; ci < rows_avail * 32; ci += T::THREADS) {
         const int row = ci >> 5, cc = ci & 31;
         const int64_t slot = g.sorted[pos0 + row];
@@ -657,7 +679,7 @@ void grouped_gemm_kernel(GemmArgs g) {
     // past kTailRows are padding; the fused outputs of those positions are the
     // zero codes and floor scales an all-zero row quantises to.
     if (nvalid <= kTailRows) {
-      gemm_tile<kTailRows, FUSED>(g, j, pos0, rows_avail, e, g0, g1, g1_store, nvalid);
+      gemm_tile<kTailRows, FUSED>(g, j, pos0, rows_avail, e, nvalid);
       if (FUSED) {
         for (int ci = kTailRows * 8 + tid; ci < rows_avail * 8; ci += T::THREADS) {
           const int row = ci >> 3, cc = ci & 7;
@@ -669,7 +691,7 @@ void grouped_gemm_kernel(GemmArgs g) {
       return;
     }
   }
-  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, g0, g1, g1_store, nvalid);
+  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
 }
 
 template <int BM, bool FUSED>
