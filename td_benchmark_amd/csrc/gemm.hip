@@ -620,10 +620,14 @@ void grouped_gemm_kernel(GemmArgs g) {
   }
   const int64_t b0 = bq - back;
   const int64_t run = back + 1 + fwd;
-  // A row tile spans ub consecutive align blocks of the run (one when BM equals
-  // the align block size); the run's `units` row tiles take its first
-  // units * NT tile ids and the rest of its ids are idle.  Only the last
-  // block of a run holds padding, so a tile's valid rows are still a prefix.
+  // A row tile spans up to ub consecutive align blocks of the run (one when BM
+  // equals the align block size); the run's `units` row tiles take its first
+  // units * NT tile ids and the rest of its ids are idle.  The run's blocks are
+  // split over its row tiles as evenly as possible, the larger tiles last:
+  // a run of three blocks in 2-block tiles becomes 1 + 2 blocks, two tiles
+  // that stream the same weight tiles at the same pace, rather than 2 + 1,
+  // a full tile and a tile of a few padded rows.  Only the last block of a run
+  // holds padding, so a tile's valid rows are still a prefix.
   const int64_t ub = BM / g.bma;
   const int64_t units = (run + ub - 1) / ub;
   const int64_t in_run = t - b0 * g.n_tiles;
@@ -635,11 +639,13 @@ void grouped_gemm_kernel(GemmArgs g) {
   const int64_t gj0 = in_run / (GG * units) * GG;
   const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
   const int64_t in_grp = in_run - gj0 * units;
-  const int64_t b = b0 + in_grp / gsz * ub;    // first align block of the tile
   const int64_t j = gj0 + in_grp % gsz;
+  const int64_t u = in_grp / gsz;               // row tile of the run
+  const int64_t base = run / units, n_short = units - run % units;  // n_short tiles of `base` blocks
+  const int64_t b = b0 + (u < n_short ? u * base : n_short * base + (u - n_short) * (base + 1));
   const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
   // tile rows that belong to this run (the rest are not read or written)
-  const int rows_avail = (int)(((b0 + run - b) < ub ? (b0 + run - b) : ub) * g.bma);
+  const int rows_avail = (int)((u < n_short ? base : base + 1) * g.bma);
 
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
