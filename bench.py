@@ -61,6 +61,34 @@ def measured_traffic(workload: str, kernel: str) -> tuple[float | None, str | No
     return None, None
 
 
+def cpu_stage_times(data, wl, D_sample, block_m: int) -> dict:
+    """The layer's quant, align and reduce stages on the host, single-threaded
+    C restatements from the oracle: quant over all T tokens, align over all S
+    slots, reduce over the first D_sample.shape[0] // k tokens' rows of the
+    GPU's D (extrapolated to T)."""
+    import numpy as np
+
+    import oracle
+
+    oracle.lib()  # load the library outside the timed calls
+    out = {}
+    x = data.x.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    ids = data.topk_ids.cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.quant_group128(x)
+    out["quant_us"] = (time.perf_counter() - t0) * 1e6
+    t0 = time.perf_counter()
+    oracle.moe_align(ids, wl.E, block_m)
+    out["align_us"] = (time.perf_counter() - t0) * 1e6
+    tr = D_sample.shape[0] // wl.top_k
+    t0 = time.perf_counter()
+    oracle.moe_reduce(D_sample[: tr * wl.top_k], tr, wl.top_k)
+    out["reduce_us"] = (time.perf_counter() - t0) * 1e6 * wl.T / max(tr, 1)
+    out["sample"] = (f"quant {wl.T}x{wl.H}, align {wl.S} slots, reduce {tr} of {wl.T} tokens "
+                     "(scaled to T); one thread each")
+    return out
+
+
 def cpu_baseline(data, wl, budget_s: float) -> dict:
     """Time oracle.golden_moe (the reference's fp32 per-expert torch CPU path,
     restated in numpy) on whole experts of this workload until ``budget_s`` of
@@ -268,6 +296,9 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(data, wl, args.cpu_budget)
+        n_rows = min(wl.T, 1024) * wl.top_k
+        D_sample = runner.D[:n_rows].view(torch.int16).cpu().numpy().view("uint16")
+        result["cpu_baseline"]["stages"] = cpu_stage_times(data, wl, D_sample, bm)
     print(json.dumps(result), flush=True)
     return 0
 
