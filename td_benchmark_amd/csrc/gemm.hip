@@ -64,6 +64,9 @@ namespace moe {
 constexpr int kXcds = 8;
 constexpr int kMaxKB = 128;  // K <= 16384
 constexpr int kTailRows = 64;  // row tiles with at most this many valid rows run the short body
+// MFMAs issued between an MFMA and the FMAs that scale its result: the VALU
+// reads a result that is complete, without hazard waits.
+constexpr int kScaleLag = 2;
 
 template <int BM>
 struct Tile {
@@ -369,15 +372,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
           ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
         }(std::make_integer_sequence<int, RA>{});
         // Column fragments double-buffered; MFMA t is issued before the scale
-        // FMAs of MFMA t-1, whose result is ready by then.  The per-row scale
-        // products a_s*b_s are formed per group; the one MFMA still pending at
-        // the group switch keeps its old products in sab_prev.
+        // FMAs of MFMA t-kScaleLag, whose result is ready by then.  The per-row
+        // scale products a_s*b_s are formed per group; the MFMAs of the first
+        // group still pending at the group switch (its last kScaleLag, rows
+        // RA-1, RA-2, ...) keep their old products in sab_prev.
+        constexpr int LG = kScaleLag;
         constexpr int NQ = 2 * T::CS;  // column fragments per step
         constexpr int NT = NQ * RA;
         v8i bq[2];
-        v4f p[2];
+        v4f p[LG + 1];
         float sab[RA][4];
-        float sab_prev[4];
+        float sab_prev[LG][4];
         bq[0] = frag_at<0>(pb0, pb1);
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
           (
@@ -386,7 +391,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
                 if constexpr (c == 0) {
                   if constexpr (gg == 1) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) sab_prev[v] = sab[RA - 1][v];
+                    for (int l = 0; l < LG; ++l)
+#pragma unroll
+                      for (int v = 0; v < 4; ++v) sab_prev[l][v] = sab[((RA - 1 - l) % RA + RA) % RA][v];
                   }
                   const float sb = smSB[gg * kMaxKB + kk];
 #pragma unroll
@@ -403,27 +410,41 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 #pragma unroll
                 for (int r = 0; r < RA; ++r) {
                   const int t = Q * RA + r;
-                  p[t & 1] = mfma_fp8(af[r], bq[Q & 1]);
-                  if (t >= 1) {
-                    const int u = t - 1, uq = u / RA, ur = u % RA;
+                  p[t % (LG + 1)] = mfma_fp8(af[r], bq[Q & 1]);
+                  if (t >= LG) {
+                    const int u = t - LG, uq = u / RA, ur = u % RA;
                     const int ug = uq / T::CS, uc = uq % T::CS;
+                    // a first-group MFMA scaled in the second group: the
+                    // (T::CS*RA - 1 - u)-th from the end of the first group
+                    const int pend = T::CS * RA - 1 - u;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
-                      const float sc = (ug == gg) ? sab[ur][v] : sab_prev[v];
-                      acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sc, acc[ur][ug][uc][v]);
+                      const float sc = (ug == gg) ? sab[ur][v] : sab_prev[pend >= 0 && pend < LG ? pend : 0][v];
+                      acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sc, acc[ur][ug][uc][v]);
                     }
                   }
                 }
               }(),
               ...);
         }(std::make_integer_sequence<int, NQ>{});
-        {  // drain the last MFMA
-          constexpr int u = NT - 1, uq = u / RA, ur = u % RA;
-          constexpr int ug = uq / T::CS, uc = uq % T::CS;
+        [&]<int... D>(std::integer_sequence<int, D...>) {  // drain the last LG MFMAs
+          (
+              [&] {
+                constexpr int u = NT - LG + D;
+                if constexpr (u >= 0) {
+                  constexpr int uq = u / RA, ur = u % RA;
+                  constexpr int ug = uq / T::CS, uc = uq % T::CS;
+                  // a first-group MFMA when the step has fewer MFMAs than LG per group
+                  constexpr int pend = T::CS * RA - 1 - u;
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            acc[ur][ug][uc][v] = __builtin_fmaf(p[u & 1][v], sab[ur][v], acc[ur][ug][uc][v]);
-        }
+                  for (int v = 0; v < 4; ++v) {
+                    const float sc = ug == 1 ? sab[ur][v] : sab_prev[pend >= 0 && pend < LG ? pend : 0][v];
+                    acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sc, acc[ur][ug][uc][v]);
+                  }
+                }
+              }(),
+              ...);
+        }(std::make_integer_sequence<int, LG>{});
       }
       stage_last = stage;
       stage = (stage == T::KS - 1) ? 0 : stage + 1;
