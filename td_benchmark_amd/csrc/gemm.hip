@@ -17,25 +17,31 @@
 // 282-284), writing FP8 codes + scales by sorted position so that the W2 GEMM
 // reads its A rows contiguously.
 //
-// Tiling: one workgroup computes BM rows (one expert block) x 256 B-rows (two
-// 128-row scale groups) with 8 waves (2 per SIMD, so one wave's MFMAs run
-// while the other waits on LDS or the barrier) for BM >= 32, and with 4 waves
-// for BM = 16 (too few rows to split).  The K step is 128 = one
-// scale block, and every K step is exactly one 16x16x128 MFMA per 16x16
-// output subtile started from zero, so the per-block scales are applied as
-// acc = fma(partial, a_s[row]*b_s[group], acc) with no second accumulator.
-// The fp32 promotion at every 128-K block also bounds the matrix core's
-// reduced-precision accumulation inside one instruction.  16-row subtiles
-// that hold only padding rows (moe_align pads every expert to BM) issue no
-// MFMA at all.
+// Tiling: one workgroup computes TM rows x 256 B-rows (two 128-row scale
+// groups).  TM is block_size_m, or 256 when the experts average at least 160
+// slots: a 256-row tile then spans consecutive align blocks of one expert,
+// split evenly over the expert's tiles, so a weight tile is fetched once per
+// up to 256 rows.  8 waves (2 per SIMD, so one wave's MFMAs run while the other
+// waits on LDS or the barrier) for TM >= 32, 4 for TM = 16; at TM = 256 they
+// are 4 x 2 waves of 64 x 128.  The K step is 128 = one scale block, and every
+// K step is exactly one 16x16x128 MFMA per 16x16 output subtile started from
+// zero, so the per-block scales are applied as acc = fma(partial,
+// a_s[row]*b_s[group], acc) (kScaleLag MFMAs later) with no second
+// accumulator.  The fp32 promotion at every 128-K block also bounds the matrix
+// core's reduced-precision accumulation inside one instruction.  16-row
+// subtiles that hold only padding rows issue no MFMA at all, and a tile with
+// at most kTailRows valid rows runs a kTailRows-row body.
 //
-// Pipeline: a 3-stage LDS ring (A BM*128 B + B 32 KiB per stage, plus the A
-// scales) filled by direct-to-LDS loads (global_load_lds_dwordx4: each lane
-// moves 16 B from its own global address -- a gathered A row -- straight into
-// LDS, no VGPR staging; addresses are a uniform base plus a fixed 32-bit lane
-// offset).  Step k waits until only step k+1's loads are in flight, passes one
-// barrier, issues step k+2's loads into the buffer freed at step k-1, then
-// computes: two K steps of memory latency hide behind MFMA work.
+// Pipeline: operand tiles go to LDS by direct-to-LDS loads
+// (global_load_lds_dwordx4: each lane moves 16 B from its own global address
+// -- a gathered A row -- straight into LDS, no VGPR staging; addresses are a
+// uniform base plus a fixed 32-bit lane offset).  Up to TM = 128 a 3-stage ring
+// (A TM*128 B + B 32 KiB per stage, plus the A scales): step k waits until only
+// step k+1's loads are in flight, passes one barrier, issues step k+2's loads
+// into the buffer freed at step k-1, then computes.  At TM = 256 three 64 KiB
+// stages exceed the LDS, so the ring has two stages and every step waits for
+// all of its loads; A rows of subtiles without a valid row are then not
+// fetched.
 //
 // LDS rows are 128 B; the 16 B chunk index of a row is XORed with
 // swz(row) = (row mod 8) ^ bit3(row), which depends only on the row's
@@ -49,9 +55,9 @@
 // instruction.
 //
 // Launch: workgroup ids are dealt round-robin to the 8 XCDs; the id -> tile map
-// gives each XCD a contiguous range of an expert-major tile order, so all M
-// blocks of one expert that read the same weight tile run together on one
-// XCD (weights leave HBM once) and an M block's A rows are shared by its
+// gives each XCD a contiguous range of an expert-major tile order, so all row
+// tiles of one expert that read the same weight tile run together on one
+// XCD (weights leave HBM once) and a row tile's A rows are shared by its
 // n-tiles in that XCD's L2.
 #include <type_traits>
 
