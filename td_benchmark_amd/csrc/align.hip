@@ -350,13 +350,11 @@ static int align_impl(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
                        rank);
   }
   // Stage the chunk counts in LDS when they fit (128 KiB of the 160 KiB).
-  static bool lds_attr = false;
-  if (!lds_attr) {
-    if (hipFuncSetAttribute((const void*)align_scan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(kAlignStageLimit * sizeof(int32_t))) != hipSuccess)
-      return kErrLaunch;
-    lds_attr = true;
-  }
+  // Set once per process (thread-safe initialisation of a function-local static).
+  static const hipError_t lds_attr_rc = hipFuncSetAttribute(
+      (const void*)align_scan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)(kAlignStageLimit * sizeof(int32_t)));
+  if (lds_attr_rc != hipSuccess) return kErrLaunch;
   const int use_lds = n_chunks * E <= kAlignStageLimit ? 1 : 0;
   hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignMaxExperts),
                      use_lds ? (size_t)(n_chunks * E * sizeof(int32_t)) : 0, st, chunk_count, n_chunks,

@@ -730,13 +730,11 @@ void grouped_gemm_kernel(GemmArgs g) {
 template <int BM, bool FUSED>
 static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   using T = Tile<BM>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)grouped_gemm_kernel<BM, FUSED>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES) != hipSuccess)
-      return kErrLaunch;
-    attr_set = true;
-  }
+  // Set once per process (a function-local static is initialised exactly once,
+  // also when several host threads make their first call together).
+  static const hipError_t attr_rc = hipFuncSetAttribute(
+      (const void*)grouped_gemm_kernel<BM, FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+  if (attr_rc != hipSuccess) return kErrLaunch;
   // Upper bound on the tile count (the real one depends on ntpp, on the device).
   const int64_t grid = (args.max_blocks * args.n_tiles + kXcds - 1) / kXcds * kXcds;
   if (grid <= 0) return kOk;

@@ -32,13 +32,81 @@ def _stream(stream: torch.cuda.Stream | None = None) -> ctypes.c_void_p:
     return ctypes.c_void_p(s.cuda_stream)
 
 
-def _need(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> None:
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be a GPU tensor")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype | None = None,
+          shape: tuple | None = None) -> None:
+    """Checks of a tensor handed to the C ABI, which receives only pointers and
+    sizes: a buffer smaller than the sizes say would be read or written out of
+    bounds on the device, so dtype and shape are checked here, before the
+    contiguity and device checks."""
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+
+
+def _blocks128(n: int) -> int:
+    return (n + 127) // 128
+
+
+def _need_weights(w: torch.Tensor, w_scale: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """FP8 expert weights [E, N, K] and their 128x128 block scales
+    [E, N/128, K/128] -> (E, N, K)."""
+    if w.dim() != 3:
+        raise ValueError(f"{name} must be [E, N, K], got {tuple(w.shape)}")
+    E, N, K = w.shape
+    _need(w, name, FP8)
+    _need(w_scale, f"{name}_scale", torch.float32, (E, _blocks128(N), _blocks128(K)))
+    return E, N, K
+
+
+def _need_routing(sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
+                  num_tokens_post_padded: torch.Tensor, block_m: int) -> None:
+    """moe_align_block_size outputs: one expert id per block of sorted positions."""
+    _need(sorted_token_ids, "sorted_token_ids", torch.int32)
+    _need(expert_ids, "expert_ids", torch.int32)
+    _need(num_tokens_post_padded, "num_tokens_post_padded", torch.int32)
+    if num_tokens_post_padded.numel() < 1:
+        raise ValueError("num_tokens_post_padded must hold one element")
+    if expert_ids.numel() * block_m < sorted_token_ids.numel():
+        raise ValueError(f"expert_ids has {expert_ids.numel()} blocks, fewer than the "
+                         f"{sorted_token_ids.numel()} sorted positions need at block size {block_m}")
+
+
+def _need_activations(A: torch.Tensor, A_scale: torch.Tensor, rows: int, cols: int | None = None) -> None:
+    """FP8 activations [>= rows, cols] and their 1x128 group scales."""
+    if A.dim() != 2:
+        raise ValueError(f"A must be 2-D, got {tuple(A.shape)}")
+    if cols is not None and A.shape[1] != cols:
+        raise ValueError(f"A has {A.shape[1]} columns, expected {cols}")
+    if A.shape[0] < rows:
+        raise ValueError(f"A has {A.shape[0]} rows, the routing reads {rows}")
+    _need(A, "A", FP8)
+    _need(A_scale, "A_scale", torch.float32, (A.shape[0], _blocks128(A.shape[1])))
+
+
+def _check_grouped_gemm(A, A_scale, B, B_scale, C, weights, sorted_token_ids, expert_ids,
+                        num_tokens_post_padded, top_k: int, a_by_pos: bool, block_m: int,
+                        row_width: int) -> int:
+    """Operands of the grouped GEMM entry points -> S, the slots (rows of C)."""
+    _need_weights(B, B_scale, "B")
+    _need_routing(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m)
+    if top_k < 1:
+        raise ValueError("top_k must be >= 1")
+    if C.numel() % row_width:
+        raise ValueError(f"C ({C.numel()} elements) is not a whole number of {row_width}-wide rows")
+    S = C.numel() // row_width
+    _need(C, "C", torch.bfloat16)
+    rows = sorted_token_ids.numel() if a_by_pos else (S + top_k - 1) // top_k
+    _need_activations(A, A_scale, rows)
+    if weights is not None:
+        _need(weights, "topk_weights", torch.float32)
+        if weights.numel() < S:
+            raise ValueError(f"topk_weights has {weights.numel()} entries for {S} slots")
+    return S
 
 
 # ---------------------------------------------------------------------------
@@ -55,10 +123,14 @@ def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128,
     per_token_group_quant_fp8 as consumed by the grouped GEMM."""
     if group_size != 128:
         raise NotImplementedError("only 1x128 activation groups are implemented")
+    if x.dim() != 2:
+        raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
     q = torch.empty((T, H), dtype=FP8, device=x.device) if out_q is None else out_q
     s = torch.empty((T, H // 128), dtype=torch.float32, device=x.device) if out_s is None else out_s
+    _need(q, "out_q", FP8, (T, H))
+    _need(s, "out_s", torch.float32, (T, H // 128))
     check(lib().moe_quant_group128(_ptr(x), T, H, _ptr(q), _ptr(s), _stream()), "moe_quant_group128")
     return q, s
 
@@ -80,13 +152,15 @@ def quantize_block128(w: torch.Tensor, out_q: torch.Tensor | None = None,
                       out_s: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """fp32 [E,N,K] -> (e4m3fn [E,N,K], scales [E,ceil(N/128),ceil(K/128)]),
     moe_bench/data/checkpoint.py:28-40 on the GPU."""
+    if w.dim() != 3:
+        raise ValueError(f"w must be [E, N, K], got {tuple(w.shape)}")
     _need(w, "w", torch.float32)
     E, N, K = w.shape
     q = torch.empty((E, N, K), dtype=FP8, device=w.device) if out_q is None else out_q
-    s = (torch.empty((E, (N + 127) // 128, (K + 127) // 128), dtype=torch.float32, device=w.device)
+    s = (torch.empty((E, _blocks128(N), _blocks128(K)), dtype=torch.float32, device=w.device)
          if out_s is None else out_s)
-    _need(q, "out_q", FP8)
-    _need(s, "out_s", torch.float32)
+    _need(q, "out_q", FP8, (E, N, K))
+    _need(s, "out_s", torch.float32, (E, _blocks128(N), _blocks128(K)))
     check(lib().moe_quant_block128(_ptr(w), E, N, K, _ptr(q), _ptr(s), _stream()), "moe_quant_block128")
     return q, s
 
@@ -176,17 +250,19 @@ def dispatch_fused_moe_kernel(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         raise NotImplementedError("zero points / bias are not on this path")
     if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
         raise NotImplementedError("only block_shape [128,128]")
-    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
-                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
-        _need(t, name)
+    if B.dim() != 3:
+        raise ValueError(f"B must be [E, N, K], got {tuple(B.shape)}")
     E, N, K = B.shape
-    S = C.numel() // N
     BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
     w = None
     if mul_routed_weight:
         if topk_weights is None:
             raise ValueError("mul_routed_weight requires topk_weights")
         w = topk_weights.contiguous().view(-1)
+    S = _check_grouped_gemm(A, A_scale, B, B_scale, C, w, sorted_token_ids, expert_ids,
+                            num_tokens_post_padded, top_k, a_by_pos, BM, N)
+    if A.shape[1] != K:
+        raise ValueError(f"A has {A.shape[1]} columns, B has K = {K}")
     check(lib().moe_grouped_gemm_tiled(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale),
                                        _ptr(sorted_token_ids), _ptr(expert_ids),
                                        _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
@@ -213,16 +289,18 @@ def invoke_moe_kernel_n_split(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         raise NotImplementedError("zero points / bias are not on this path")
     if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
         raise NotImplementedError("only block_shape [128,128]")
-    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
-                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
-        _need(t, name)
+    if B.dim() != 3:
+        raise ValueError(f"B must be [E, N, K], got {tuple(B.shape)}")
     E, full_N, K = B.shape
     N_chunk = full_N - N_offset if N_chunk is None else N_chunk
-    S = C.numel() // full_N
     BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
-    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
     if mul_routed_weight and topk_weights is None:
         raise ValueError("mul_routed_weight requires topk_weights")
+    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
+    S = _check_grouped_gemm(A, A_scale, B, B_scale, C, w, sorted_token_ids, expert_ids,
+                            num_tokens_post_padded, top_k, a_by_pos, BM, full_N)
+    if A.shape[1] != K:
+        raise ValueError(f"A has {A.shape[1]} columns, B has K = {K}")
     check(lib().moe_grouped_gemm_n_split(_ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids),
                                          _ptr(expert_ids), _ptr(num_tokens_post_padded), _ptr(w), S, top_k,
                                          1 if a_by_pos else 0, full_N, N_offset, N_chunk, K, E, BM,
@@ -247,17 +325,17 @@ def invoke_moe_kernel_k_split(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         raise NotImplementedError("only fp8_w8a8 block-scaled GEMM is implemented")
     if block_shape is not None and list(block_shape) != BLOCK_SHAPE:
         raise NotImplementedError("only block_shape [128,128]")
-    for name, t in (("A", A), ("B", B), ("C", C), ("A_scale", A_scale), ("B_scale", B_scale),
-                    ("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
-        _need(t, name)
+    if B.dim() != 3:
+        raise ValueError(f"B must be [E, N, K], got {tuple(B.shape)}")
     E, N, full_K = B.shape
     K_chunk = full_K - K_offset if K_chunk is None else K_chunk
     a_k = K_offset if A_K_offset < 0 else A_K_offset
-    S = C.numel() // N
     BM = int((config or {}).get("BLOCK_SIZE_M", 0)) or _block_m_from(sorted_token_ids, expert_ids)
-    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
     if mul_routed_weight and topk_weights is None:
         raise ValueError("mul_routed_weight requires topk_weights")
+    w = topk_weights.contiguous().view(-1) if mul_routed_weight else None
+    S = _check_grouped_gemm(A, A_scale, B, B_scale, C, w, sorted_token_ids, expert_ids,
+                            num_tokens_post_padded, top_k, a_by_pos, BM, N)
     check(lib().moe_grouped_gemm_k_split(_ptr(A), _ptr(A_scale), A.shape[-1], a_k, _ptr(B), _ptr(B_scale),
                                          _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(num_tokens_post_padded),
                                          _ptr(w), S, top_k, 1 if a_by_pos else 0, N, full_K, K_offset, K_chunk,
@@ -281,13 +359,19 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
     """W13 GEMM + SiLU*up + 1x128 quant of h, outputs by sorted position:
     (hq [max_padded, I] e4m3fn, hs [max_padded, I/128] fp32).  ``tile_m`` as
     for dispatch_fused_moe_kernel."""
-    E, N2, H = w13.shape
+    E, N2, H = _need_weights(w13, w13_scale, "w13")
     I = N2 // 2
+    _need_routing(sorted_token_ids, expert_ids, num_tokens_post_padded, block_size_m)
+    if top_k < 1:
+        raise ValueError("top_k must be >= 1")
+    _need_activations(Aq, A_scale, (num_slots + top_k - 1) // top_k, H)
     max_padded = sorted_token_ids.numel()
     if hq is None:
         hq = torch.empty((max_padded, I), dtype=FP8, device=Aq.device)
     if hs is None:
         hs = torch.empty((max_padded, I // 128), dtype=torch.float32, device=Aq.device)
+    _need(hq, "hq", FP8, (max_padded, I))
+    _need(hs, "hs", torch.float32, (max_padded, _blocks128(I)))
     check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
                                               _ptr(sorted_token_ids), _ptr(expert_ids),
                                               _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
@@ -305,9 +389,9 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
     """torch.ops._C.silu_and_mul(out, x): out[r,j] = silu(x[r,j]) * x[r,I+j]
     (overlap/overlap_forward.py:277-279)."""
     _need(x, "x", torch.bfloat16)
-    _need(out, "out", torch.bfloat16)
     R = x.numel() // x.shape[-1]
     I = x.shape[-1] // 2
+    _need(out, "out", torch.bfloat16, tuple(x.shape[:-1]) + (I,))
     check(lib().moe_silu_and_mul(_ptr(x), R, I, _ptr(out), _stream()), "moe_silu_and_mul")
 
 
@@ -321,6 +405,8 @@ def silu_mul_quant_group128(x: torch.Tensor, out_q: torch.Tensor | None = None,
     I = x.shape[-1] // 2
     q = torch.empty((R, I), dtype=FP8, device=x.device) if out_q is None else out_q
     s = torch.empty((R, I // 128), dtype=torch.float32, device=x.device) if out_s is None else out_s
+    _need(q, "out_q", FP8, (R, I))
+    _need(s, "out_s", torch.float32, (R, I // 128))
     check(lib().moe_silu_mul_quant_group128(_ptr(x), R, I, _ptr(q), _ptr(s), _stream()),
           "moe_silu_mul_quant_group128")
     return q, s
@@ -333,9 +419,13 @@ def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int,
     With ``addend`` ([T, H] bf16, the shared expert's output) the bf16 sum is
     added to it in the same pass, as ``result + shared(hidden)`` does
     (schemes/vllm_tp.py:62-63)."""
+    if out.dim() != 2:
+        raise ValueError(f"out must be [T, H], got {tuple(out.shape)}")
+    T, H = out.shape
+    if D.numel() != T * top_k * H:
+        raise ValueError(f"D has {D.numel()} elements, [T*top_k, H] = [{T * top_k}, {H}] needs {T * top_k * H}")
     _need(D, "D", torch.bfloat16)
     _need(out, "out", torch.bfloat16)
-    T, H = out.shape
     if addend is None:
         check(lib().moe_reduce_topk(_ptr(D), T, top_k, H, _ptr(out), _stream()), "moe_reduce_topk")
     else:
@@ -392,11 +482,10 @@ class SharedExpertRunner:
 
     def __init__(self, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, max_tokens: int, block_size_m: int | None = None):
-        for name, t in (("w1", w1), ("w2", w2)):
-            _need(t, name, FP8)
-        if w1.shape[0] != 1 or w2.shape[0] != 1:
+        E1, N2, H = _need_weights(w1, w1_scale, "w1")
+        _need_weights(w2, w2_scale, "w2")
+        if E1 != 1 or w2.shape[0] != 1:
             raise ValueError("the shared expert has exactly one expert")
-        _, N2, H = w1.shape
         if w2.shape != (1, H, N2 // 2):
             raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w1 {tuple(w1.shape)}")
         self.w1, self.w1_scale, self.w2, self.w2_scale = w1, w1_scale, w2, w2_scale
@@ -432,9 +521,11 @@ class SharedExpertRunner:
                 raise ValueError(f"input_scale rows {input_scale.shape[0]} do not match input rows {rows}")
             q, s = x, input_scale
         else:
+            if tuple(x.shape) != (rows, self.H):
+                raise ValueError(f"x must be [rows, {self.H}], got {tuple(x.shape)}")
             q, s = per_token_group_quant_fp8(x, out_q=self.q[:rows], out_s=self.s[:rows])
-        _need(q, "x", FP8)
-        _need(s, "input_scale", torch.float32)
+        _need(q, "x", FP8, (rows, self.H))
+        _need(s, "input_scale", torch.float32, (rows, self.H // 128))
         a = self._align_for(rows)
         check(lib().moe_gemm_w13_silu_quant(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
                                             _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
@@ -461,11 +552,8 @@ class FusedExpertsRunner:
                  shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None,
                  global_num_experts: int | None = None, expert_map: torch.Tensor | None = None,
                  tile_m: int = 0):
-        for name, t in (("w13", w13), ("w2", w2)):
-            _need(t, name, FP8)
-        _need(w13_scale, "w13_scale", torch.float32)
-        _need(w2_scale, "w2_scale", torch.float32)
-        E, N2, H = w13.shape
+        E, N2, H = _need_weights(w13, w13_scale, "w13")
+        _need_weights(w2, w2_scale, "w2")
         if w2.shape != (E, H, N2 // 2):
             raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
         self.E, self.H, self.I, self.T, self.top_k = E, H, N2 // 2, num_tokens, top_k
@@ -527,6 +615,8 @@ class FusedExpertsRunner:
 
     def stage_w2(self, topk_weights: torch.Tensor) -> None:
         _need(topk_weights, "topk_weights", torch.float32)
+        if topk_weights.numel() != self.S:
+            raise ValueError(f"topk_weights has {topk_weights.numel()} entries for {self.S} slots")
         a = self.align
         check(lib().moe_grouped_gemm_tiled(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
                                            _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
