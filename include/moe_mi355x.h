@@ -200,6 +200,21 @@ int moe_reduce_topk(const void* D_bf16, int64_t T, int32_t top_k, int64_t H, voi
 int moe_reduce_topk_add(const void* D_bf16, const void* addend_bf16, int64_t T, int32_t top_k,
                         int64_t H, void* y_bf16, void* stream);
 
+/* FP8 reduce-scatter combine -- the dequantise-and-sum of the FP8 chunks a
+ * rank receives in the FP8-compressed reduce-scatter leg, replacing
+ * `(fp8.to(float32) * scale.repeat_interleave(128)).sum(dim=0).to(bfloat16)`
+ * (overlap/overlap_forward.py:932-944; the senders quantise with
+ * moe_quant_group128, :900-905):
+ *   out[m, n] = bf16( sum_{r<R} float(q[r, m, n]) * s[r*M + m, n/128] ),
+ * each product rounded to fp32, the sum in fp32 over ascending r.
+ * q [R, M, N] e4m3fn (R ranks' chunks of M rows, contiguous); s fp32 with a
+ * row of scale_ld >= ceil(N/128) entries per (r, m); out bf16 with rows of
+ * out_ld >= N elements (a column slice of a wider output may be written in
+ * place).  N % 16 == 0, out_ld % 8 == 0, q and out 16-byte aligned;
+ * 1 <= R <= 64. */
+int moe_fp8_dequant_sum(const void* q_fp8, const float* scales, int64_t R, int64_t M, int64_t N,
+                        int64_t scale_ld, void* out_bf16, int64_t out_ld, void* stream);
+
 /* Test hook (no reference counterpart): one 16x16x128 FP8 MFMA through the
  * GEMM's own LDS swizzle, fragment loader and output mapping.
  * A [16,128], B [16,128] e4m3fn -> C [16,16] fp32 = A . B^T. */

@@ -80,6 +80,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_grouped_gemm.argtypes = [P, P, P, P, P, P, i32, i32, i64, i32, i64, i64, i32, P, P, P]
     L.oracle_silu_and_mul.argtypes = [P, i64, i64, P]
     L.oracle_moe_reduce.argtypes = [P, i64, i32, i64, P]
+    L.oracle_fp8_dequant_sum.argtypes = [P, P, i64, i64, i64, i64, P, i64]
 
 
 def _ptr(a: np.ndarray | None) -> ctypes.c_void_p | None:
@@ -246,6 +247,20 @@ def moe_reduce(D_bf16: np.ndarray, T: int, k: int) -> np.ndarray:
     y = np.empty((T, H), np.uint16)
     lib().oracle_moe_reduce(_ptr(D), T, k, H, _ptr(y))
     return y
+
+
+def fp8_dequant_sum(q: np.ndarray, s: np.ndarray, out_ld: int | None = None) -> np.ndarray:
+    """Combine of the FP8 reduce-scatter leg: q [R, M, N] e4m3 codes, s
+    [R*M, G >= ceil(N/128)] fp32 -> [M, N] bf16 bits (or [M, out_ld] with
+    the first N columns written).  Reference: overlap/overlap_forward.py:
+    932-944."""
+    q = _c(q, np.uint8)
+    s = _c(s, np.float32)
+    R, M, N = q.shape
+    ld = N if out_ld is None else out_ld
+    out = np.zeros((M, ld), np.uint16)
+    lib().oracle_fp8_dequant_sum(_ptr(q), _ptr(s), R, M, N, s.shape[1], _ptr(out), ld)
+    return out
 
 
 def moe_layer_stages(x_bf16, topk_ids, topk_w, w13_q, w13_s, w2_q, w2_s, BM):

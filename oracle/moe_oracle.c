@@ -310,3 +310,27 @@ void oracle_moe_reduce(const uint16_t* D, int64_t T, int32_t k, int64_t H, uint1
             y[t * H + n] = oracle_f32_to_bf16(acc);
         }
 }
+
+/* ---------------------------------------------------------------------------
+ * Combine of the FP8-compressed reduce-scatter leg,
+ * overlap/overlap_forward.py:932-944:
+ *   fp8_f32 = fp8_3d.to(float32); scale_expanded = scale_3d.repeat_interleave(128)
+ *   out = (fp8_f32 * scale_expanded).sum(dim=0).to(bfloat16)
+ * restated as out[m, n] = bf16( sum_r (float(q[r, m, n]) * s[(r*M + m)*ld + n/128]) ),
+ * each product rounded to fp32 before it is added (the reference forms the
+ * product tensor first), the sum in fp32 over ascending r.
+ * q: e4m3 [R, M, N]; out: bf16 bits with rows of out_ld elements.
+ * ------------------------------------------------------------------------- */
+void oracle_fp8_dequant_sum(const uint8_t* q, const float* s, int64_t R, int64_t M, int64_t N,
+                            int64_t scale_ld, uint16_t* out, int64_t out_ld) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            float acc = 0.0f;
+            for (int64_t r = 0; r < R; ++r) {
+                /* built with -ffp-contract=off: the product is rounded before the add */
+                float p = oracle_e4m3_to_f32(q[(r * M + m) * N + n]) * s[(r * M + m) * scale_ld + n / 128];
+                acc = acc + p;
+            }
+            out[m * out_ld + n] = oracle_f32_to_bf16(acc);
+        }
+}

@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                                 _P]),
     "moe_silu_mul_quant_group128": (ctypes.c_int, [_P, _i64, _i64, _P, _P, _P]),
     "moe_reduce_topk_add": (ctypes.c_int, [_P, _P, _i64, _i32, _i64, _P, _P]),
+    "moe_fp8_dequant_sum": (ctypes.c_int, [_P, _P, _i64, _i64, _i64, _i64, _P, _i64, _P]),
     "moe_gemm_w13_silu_quant": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
                                                _i64, _i32, _i32, _i64, _P, _P, _P]),
     "moe_gemm_w13_silu_quant_tiled": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,

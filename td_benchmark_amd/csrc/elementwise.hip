@@ -11,6 +11,13 @@
 // math (torch.ops._C.silu_and_mul, overlap/overlap_forward.py:277-279).  The
 // fused W13 kernel performs the same arithmetic in its epilogue; this op
 // serves the unfused chain.
+//
+// moe_fp8_dequant_sum: the combine of the FP8-compressed reduce-scatter leg
+// (overlap/overlap_forward.py:932-944): out[m, n] = bf16( sum_r
+// float(q[r, m, n]) * s[r, m, n/128] ), the product rounded to fp32 (no fused
+// multiply-add), the sum in fp32 over ascending r.  HBM-bound: R*N + 4*R*N/128
+// bytes read and 2*N written per row; each thread owns 16 columns of one row
+// and keeps up to kDequantBatch ranks' loads in flight.
 #include "common.hpp"
 
 namespace moe {
@@ -61,6 +68,61 @@ __global__ __launch_bounds__(256) void reduce_topk_kernel(const uint16_t* __rest
     out[j] = (int)(lo | (hi << 16));
   }
   __builtin_nontemporal_store(out, reinterpret_cast<v4i*>(y + t * H + cc * 8));
+}
+
+constexpr int kMaxRanks = 64;
+constexpr int kDequantBatch = 8;
+
+__global__ __launch_bounds__(256) void fp8_dequant_sum_kernel(const uint8_t* __restrict__ q,
+                                                              const float* __restrict__ s,
+                                                              uint16_t* __restrict__ out, int R,
+                                                              int64_t M, int64_t N, int64_t scale_ld,
+                                                              int64_t out_ld) {
+#pragma clang fp contract(off)
+  const int64_t cpr = N / 16;  // 16-column chunks per row
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * cpr) return;
+  const int64_t m = idx / cpr, c = idx % cpr;
+  const int64_t grp = c / 8;  // 128-column scale group of the chunk
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  for (int r0 = 0; r0 < R; r0 += kDequantBatch) {
+    v4i qv[kDequantBatch];
+    float sc[kDequantBatch];
+#pragma unroll
+    for (int b = 0; b < kDequantBatch; ++b) {
+      if (r0 + b < R) {
+        const int64_t row = (int64_t)(r0 + b) * M + m;
+        qv[b] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(q + row * N + c * 16));
+        sc[b] = s[row * scale_ld + grp];
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kDequantBatch; ++b) {
+      if (r0 + b < R) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int word = qv[b][w];
+          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);  // bytes 0, 1
+          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);   // bytes 2, 3
+          acc[4 * w + 0] = acc[4 * w + 0] + lo[0] * sc[b];
+          acc[4 * w + 1] = acc[4 * w + 1] + lo[1] * sc[b];
+          acc[4 * w + 2] = acc[4 * w + 2] + hi[0] * sc[b];
+          acc[4 * w + 3] = acc[4 * w + 3] + hi[1] * sc[b];
+        }
+      }
+    }
+  }
+  v4i o0, o1;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    o0[w] = (int)pack_bf16x2(acc[2 * w], acc[2 * w + 1]);
+    o1[w] = (int)pack_bf16x2(acc[8 + 2 * w], acc[8 + 2 * w + 1]);
+  }
+  uint16_t* dst = out + m * out_ld + c * 16;
+  __builtin_nontemporal_store(o0, reinterpret_cast<v4i*>(dst));
+  __builtin_nontemporal_store(o1, reinterpret_cast<v4i*>(dst + 8));
 }
 
 __global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __restrict__ c,
@@ -141,5 +203,18 @@ extern "C" int moe_silu_and_mul(const void* c_bf16, int64_t R, int64_t I, void* 
   const int64_t blocks = (R * (I / 8) + 255) / 256;
   hipLaunchKernelGGL(silu_and_mul_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)c_bf16, (uint16_t*)h_bf16, R, I);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_fp8_dequant_sum(const void* q_fp8, const float* scales, int64_t R, int64_t M, int64_t N,
+                                   int64_t scale_ld, void* out_bf16, int64_t out_ld, void* stream) {
+  if (R < 1 || R > kMaxRanks || M < 0 || N < 0) return kErrBadShape;
+  if (M == 0 || N == 0) return kOk;
+  if (!q_fp8 || !scales || !out_bf16) return kErrNullPointer;
+  if (N % 16 != 0 || scale_ld < (N + 127) / 128 || out_ld < N || out_ld % 8 != 0) return kErrBadShape;
+  if (!aligned16(q_fp8) || !aligned16(out_bf16)) return kErrBadShape;
+  const int64_t blocks = (M * (N / 16) + 255) / 256;
+  hipLaunchKernelGGL(fp8_dequant_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)q_fp8, scales, (uint16_t*)out_bf16, (int)R, M, N, scale_ld, out_ld);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

@@ -437,6 +437,54 @@ def moe_sum(D: torch.Tensor, out: torch.Tensor, top_k: int,
     return out
 
 
+def fp8_dequant_sum(recv_q: torch.Tensor, recv_s: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """The combine of the FP8-compressed reduce-scatter leg
+    (overlap/overlap_forward.py:932-944): the R ranks' FP8 chunks of this
+    rank's M rows, recv_q [R, M, N] e4m3fn, with their 1x128 scales recv_s
+    ([R, M, G] or [R*M, G] fp32, G >= ceil(N/128); a column slice of a wider
+    buffer is read in place) ->
+    out [M, N] bf16 = sum over ranks of float(q) * scale (fp32 products, fp32
+    sum over ascending rank, one bf16 rounding).  ``out`` may be a column
+    slice of a wider [M, *] tensor (the reference's torch.cat of the chunk
+    outputs, :946, then needs no copy).  The senders quantise with
+    per_token_group_quant_fp8 (:900-905)."""
+    if recv_q.dim() != 3:
+        raise ValueError(f"recv_q must be [R, M, N], got {tuple(recv_q.shape)}")
+    R, M, N = recv_q.shape
+    groups = _blocks128(N)
+    if recv_s.dim() == 3:
+        if tuple(recv_s.shape[:2]) != (R, M) or recv_s.shape[2] < groups:
+            raise ValueError(f"recv_s must be [{R}, {M}, >= {groups}], got {tuple(recv_s.shape)}")
+        if recv_s.stride(2) != 1 or recv_s.stride(0) != M * recv_s.stride(1):
+            raise ValueError("recv_s rows must be evenly strided with unit column stride")
+        scale_ld = recv_s.stride(1)
+    elif recv_s.dim() == 2:
+        if recv_s.shape[0] != R * M or recv_s.shape[1] < groups:
+            raise ValueError(f"recv_s must be [{R * M}, >= {groups}], got {tuple(recv_s.shape)}")
+        if recv_s.stride(1) != 1:
+            raise ValueError("recv_s must have unit column stride")
+        scale_ld = recv_s.stride(0)
+    else:
+        raise ValueError(f"recv_s must be 2-D or 3-D, got {tuple(recv_s.shape)}")
+    if recv_s.dtype != torch.float32:
+        raise TypeError(f"recv_s must be torch.float32, got {recv_s.dtype}")
+    if not recv_s.is_cuda:
+        raise ValueError("recv_s must be a GPU tensor")
+    _need(recv_q, "recv_q", FP8)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=recv_q.device)
+    if out.dtype != torch.bfloat16:
+        raise TypeError(f"out must be torch.bfloat16, got {out.dtype}")
+    if tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"out must be [{M}, {N}] with unit column stride, got {tuple(out.shape)}")
+    if not out.is_cuda:
+        raise ValueError("out must be a GPU tensor")
+    check(lib().moe_fp8_dequant_sum(_ptr(recv_q), _ptr(recv_s), R, M, N, scale_ld, _ptr(out),
+                                    out.stride(0) if M > 1 else N, _stream()), "moe_fp8_dequant_sum")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # A4 -- tile configuration
 # ---------------------------------------------------------------------------
