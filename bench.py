@@ -143,6 +143,7 @@ def cpu_baseline(data, wl, budget_s: float) -> dict:
                    f"{int((counts > 0).sum())} active experts ({slots} of {wl.S} slots), {t_total:.1f} s"),
         "layer_us_extrapolated": t_total / max(slots, 1) * wl.S * 1e6,
         "cpu_model": model,
+        "host_cpus": os.cpu_count(),
     }
 
 
