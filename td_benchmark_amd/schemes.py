@@ -104,7 +104,7 @@ SPEC = SchemeSpec(
     act_quant="group128",
     requires_nvshmem=False,
     tunables_schema={
-        "block_m": TunableSpec(int, 0, "moe_align block size (16/32/64/128); 0 picks from rows per expert"),
+        "block_m": TunableSpec(int, 0, "moe_align block size (16/32/64/128/256); 0 picks from rows per expert"),
         "n_chunks": TunableSpec(int, 1, "token chunks pipelined over n_streams HIP streams"),
         "n_streams": TunableSpec(int, 1, "HIP streams for the chunk pipeline (default priority)"),
     },
