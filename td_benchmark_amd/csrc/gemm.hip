@@ -35,10 +35,12 @@
 // Pipeline: operand tiles go to LDS by direct-to-LDS loads
 // (global_load_lds_dwordx4: each lane moves 16 B from its own global address
 // -- a gathered A row -- straight into LDS, no VGPR staging; addresses are a
-// uniform base plus a fixed 32-bit lane offset).  Up to TM = 128 a 3-stage ring
-// (A TM*128 B + B 32 KiB per stage, plus the A scales): step k waits until only
-// step k+1's loads are in flight, passes one barrier, issues step k+2's loads
-// into the buffer freed at step k-1, then computes.  At TM = 256 three 64 KiB
+// uniform base plus a fixed 32-bit lane offset).  For TM = 64 and 128 a 3-stage
+// ring (A TM*128 B + B 32 KiB per stage, plus the A scales): step k waits until
+// only step k+1's loads are in flight, passes one barrier, issues step k+2's
+// loads into the buffer freed at step k-1, then computes.  TM = 16 and 32 (the
+// weight-streaming decode tiles) keep a 4-stage ring, two younger stages in
+// flight.  At TM = 256 three 64 KiB
 // stages exceed the LDS, so the ring has two stages and every step waits for
 // all of its loads; A rows of subtiles without a valid row are then not
 // fetched.
@@ -80,8 +82,9 @@ struct Tile {
   static constexpr int THREADS = 64 * NW;
   // waves along M: 4 x 2 waves of 64 x 128 at BM = 256 (fewer LDS bytes per MFMA)
   static constexpr int WM = BM == 256 ? 4 : ((NW == 8 || BM == 128) ? 2 : 1);
-  // LDS ring depth: three 64 KiB stages of the 256-row tile exceed 160 KiB
-  static constexpr int KS = BM == 256 ? 2 : 3;
+  // LDS ring depth: three 64 KiB stages of the 256-row tile exceed 160 KiB;
+  // the 34-36 KiB stages of the 16- and 32-row tiles (weight streaming) fit four
+  static constexpr int KS = BM == 256 ? 2 : (BM <= 32 ? 4 : 3);
   static constexpr int WN = NW / WM;              // waves along N
   static constexpr int RS = BM / WM / 16;         // 16-row subtiles per wave
   static constexpr int CS = 8 / WN;               // 16-col subtiles per wave per group
@@ -110,7 +113,7 @@ struct Tile {
   static constexpr int LDS_BYTES = OFF_ROW + BM * 8;
   static_assert(BM * 512 <= OFF_SA, "bf16 output staging must fit in the operand ring");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-  static_assert(VM < 16, "vmcnt immediate");
+  static_assert(VM * (KS - 2) < 64, "vmcnt immediate");
 };
 
 struct GemmArgs {
@@ -341,7 +344,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   const int sa_lane = row_base + 4 * kseg;
 
   issue_stage(0, 0, bg0, bg1);
-  if (T::KS == 3 && KB > 1) issue_stage(1, 1, bg0, bg1);
+#pragma unroll
+  for (int st = 1; st < T::KS - 1; ++st)
+    if (st < KB) issue_stage(st, st, bg0, bg1);
   if (tid < 2 * KB) smSB[(tid / KB) * kMaxKB + tid % KB] = sb_val;
   wait_lgkm0();  // the weight-scale ds_writes
 
@@ -361,8 +366,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     constexpr int RA = decltype(ra_c)::value;  // active 16-row subtiles of this wave
     int stage = 0;
     for (int kk = 0; kk < KB; ++kk) {
-      // Step kk's loads complete; with three stages step kk+1's may stay in flight.
-      if (T::KS == 3 && kk + 1 < KB) wait_vmcnt<T::VM>(); else wait_vmcnt<0>();
+      // Step kk's loads complete; the younger stages' loads (up to KS - 2 of
+      // them, as many as were issued) may stay in flight.
+      if (T::KS == 4 && kk + 2 < KB) wait_vmcnt<2 * T::VM>();
+      else if (T::KS >= 3 && kk + 1 < KB) wait_vmcnt<T::VM>();
+      else wait_vmcnt<0>();
       block_barrier();
       // The buffer read at step kk-1 is free once every wave has passed the barrier.
       if (kk + T::KS - 1 < KB) issue_stage(kk + T::KS - 1, stage == 0 ? T::KS - 1 : stage - 1, bg0, bg1);
