@@ -212,6 +212,127 @@ MOE_DEVICE void groups_of(const GemmArgs& g, int64_t j, int64_t& g0, int64_t& g1
   }
 }
 
+// The epilogue of one tile, shared by both K-loop bodies: SiLU*up and the
+// 1x128 quant of h written by sorted position (fused W13), or the bf16 rows
+// (routed weights applied) written by slot.  `staging` is LDS for BM x 256 B.
+// Output element (r, gg, c, v) of a lane: row = row_base + r*16 + 4*kseg + v,
+// column (within group gg) = col_base + c*16 + fr.
+template <int BM, bool FUSED>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile<BM>::RS][2][Tile<BM>::CS],
+                                              int64_t j, int64_t pos0, int rows_avail, int64_t g0,
+                                              int64_t g1, bool g1_store, uint8_t* staging, float* smRed,
+                                              const int32_t* smSlot, const float* smW) {
+  using T = Tile<BM>;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / T::WN;
+  const int wn = wave % T::WN;
+  const int row_base = wm * T::RS * 16;
+  const int col_base = wn * T::CS * 16;
+  const int fr = lane & 15;
+  const int kseg = lane >> 4;
+  if constexpr (FUSED) {
+    float pmax[T::RS][4];
+#pragma unroll
+    for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) pmax[r][v] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+      for (int c = 0; c < T::CS; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t gu = pack_bf16x2(acc[r][0][c][v], acc[r][1][c][v]);
+          const float h = silu_mul_bf16(lo_bf16(gu), hi_bf16(gu));
+          acc[r][0][c][v] = h;
+          pmax[r][v] = fmaxf(pmax[r][v], fabsf(h));
+        }
+#pragma unroll
+    for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float m = pmax[r][v];
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        m = fmaxf(m, __shfl_xor(m, 4));
+        m = fmaxf(m, __shfl_xor(m, 8));
+        if (fr == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
+      }
+    __syncthreads();
+    uint8_t* stage_out = staging;  // [BM][128] fp8 codes
+    const int64_t hgroups = g.I / 128;
+#pragma unroll
+    for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = row_base + r * 16 + 4 * kseg + v;
+        float amax = 0.0f;
+#pragma unroll
+        for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
+        const float sc = group_scale(amax);
+        const float inv = 1.0f / sc;
+        if (wn == 0 && fr == 0 && row < rows_avail) g.hs[(pos0 + row) * hgroups + j] = sc;
+#pragma unroll
+        for (int c = 0; c < T::CS; c += 2) {
+          const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
+          const float q1 = clamp_fp8(div_by(acc[r][0][c + 1][v], sc, inv));
+          const uint32_t pk = pack4_e4m3(q0, q1, 0.0f, 0.0f);
+          stage_out[row * 128 + col_base + c * 16 + fr] = (uint8_t)(pk & 0xFF);
+          stage_out[row * 128 + col_base + (c + 1) * 16 + fr] = (uint8_t)((pk >> 8) & 0xFF);
+        }
+      }
+    __syncthreads();
+    for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
+      const int row = ci >> 3, cc = ci & 7;
+      *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) =
+          *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
+    }
+  } else {
+    // One 128-column group per pass, staged as [BM][128] bf16.
+    uint16_t* stage_out = reinterpret_cast<uint16_t*>(staging);
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      if (gg == 1 && !g1_store) break;
+      if (gg == 1) __syncthreads();  // the first pass's stores have read the staging
+#pragma unroll
+      for (int r = 0; r < T::RS; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = row_base + r * 16 + 4 * kseg + v;
+          const float w = smW[row];
+#pragma unroll
+          for (int c = 0; c < T::CS; ++c) {
+            float val = acc[r][gg][c][v];
+            if (g.topk_w) val = val * w;
+            stage_out[row * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
+          }
+        }
+      __syncthreads();
+      const int64_t n0 = (gg ? g1 : g0) * 128;
+      for (int ci = tid; ci < BM * 16; ci += T::THREADS) {
+        const int row = ci >> 4, cc = ci & 15;
+        const int64_t slot = smSlot[row];
+        if (slot >= g.S) continue;
+        v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 8);
+        v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n0 + cc * 8);
+        if (g.accumulate) {
+          // K-split accumulation: the bf16 partial is added to the bf16 C of the
+          // earlier chunks and rounded again.
+          const v4i old = *dst;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
+            val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
+          }
+        }
+        *dst = val;
+      }
+    }
+  }
+}
+
 // The K loop and epilogue of one tile: n-tile j of rows [pos0, pos0 +
 // rows_avail) of the sorted order (a prefix of nvalid of them hold slots) of
 // expert e, with BM-row operand tiles.  A body with BM smaller than the tile
@@ -473,110 +594,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   }
   block_barrier();  // every wave is done with the last step's buffer; stage the output there
 
-  // ---- epilogues ----------------------------------------------------------
-  // Output element (r, gg, c, v) of this lane: row = row_base + r*16 + 4*kseg + v,
-  // column (within group gg) = col_base + c*16 + fr.
-  if constexpr (FUSED) {
-    float pmax[T::RS][4];
-#pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) pmax[r][v] = 0.0f;
-#pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int c = 0; c < T::CS; ++c)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t gu = pack_bf16x2(acc[r][0][c][v], acc[r][1][c][v]);
-          const float h = silu_mul_bf16(lo_bf16(gu), hi_bf16(gu));
-          acc[r][0][c][v] = h;
-          pmax[r][v] = fmaxf(pmax[r][v], fabsf(h));
-        }
-#pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float m = pmax[r][v];
-        m = fmaxf(m, __shfl_xor(m, 1));
-        m = fmaxf(m, __shfl_xor(m, 2));
-        m = fmaxf(m, __shfl_xor(m, 4));
-        m = fmaxf(m, __shfl_xor(m, 8));
-        if (fr == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
-      }
-    __syncthreads();
-    uint8_t* stage_out = smem + stage_last * T::STAGE;  // [BM][128] fp8 codes
-    const int64_t hgroups = g.I / 128;
-#pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = row_base + r * 16 + 4 * kseg + v;
-        float amax = 0.0f;
-#pragma unroll
-        for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
-        const float sc = group_scale(amax);
-        const float inv = 1.0f / sc;
-        if (wn == 0 && fr == 0 && row < rows_avail) g.hs[(pos0 + row) * hgroups + j] = sc;
-#pragma unroll
-        for (int c = 0; c < T::CS; c += 2) {
-          const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
-          const float q1 = clamp_fp8(div_by(acc[r][0][c + 1][v], sc, inv));
-          const uint32_t pk = pack4_e4m3(q0, q1, 0.0f, 0.0f);
-          stage_out[row * 128 + col_base + c * 16 + fr] = (uint8_t)(pk & 0xFF);
-          stage_out[row * 128 + col_base + (c + 1) * 16 + fr] = (uint8_t)((pk >> 8) & 0xFF);
-        }
-      }
-    __syncthreads();
-    for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
-      const int row = ci >> 3, cc = ci & 7;
-      *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) =
-          *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
-    }
-  } else {
-    // One 128-column group per pass, staged as [BM][128] bf16 in the last
-    // step's buffer (BM*256 B fits in a stage for every BM).
-    static_assert(BM * 256 <= T::STAGE, "one group's bf16 output must fit in a stage");
-    uint16_t* stage_out = reinterpret_cast<uint16_t*>(smem + stage_last * T::STAGE);
-#pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      if (gg == 1 && !g1_store) break;
-      if (gg == 1) __syncthreads();  // the first pass's stores have read the staging
-#pragma unroll
-      for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = row_base + r * 16 + 4 * kseg + v;
-          const float w = smW[row];
-#pragma unroll
-          for (int c = 0; c < T::CS; ++c) {
-            float val = acc[r][gg][c][v];
-            if (g.topk_w) val = val * w;
-            stage_out[row * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
-          }
-        }
-      __syncthreads();
-      const int64_t n0 = (gg ? g1 : g0) * 128;
-      for (int ci = tid; ci < BM * 16; ci += T::THREADS) {
-        const int row = ci >> 4, cc = ci & 15;
-        const int64_t slot = smSlot[row];
-        if (slot >= g.S) continue;
-        v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 8);
-        v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n0 + cc * 8);
-        if (g.accumulate) {
-          // K-split accumulation: the bf16 partial is added to the bf16 C of the
-          // earlier chunks and rounded again.
-          const v4i old = *dst;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
-            val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
-          }
-        }
-        *dst = val;
-      }
-    }
-  }
+  static_assert(BM * 256 <= T::STAGE, "one group's bf16 output must fit in a stage");
+  tile_epilogue<BM, FUSED>(g, acc, j, pos0, rows_avail, g0, g1, g1_store, smem + stage_last * T::STAGE, smRed,
+                           smSlot, smW);
 
 }
 
