@@ -21,6 +21,10 @@ from moe_cases import bf16_bits, make_case, to_gpu
 pytestmark = pytest.mark.gpu
 
 
+# (T, E, k, BM): 32-row tiles, and 256-row tiles over 64-row blocks (S >= 160*E)
+SETUPS = {"short": dict(T=150, E=6, k=3, BM=32), "tall": dict(T=700, E=4, k=2, BM=64)}
+
+
 def _setup(T=150, H=512, I=384, E=6, k=3, BM=32, seed=21):
     import torch
 
@@ -34,14 +38,15 @@ def _setup(T=150, H=512, I=384, E=6, k=3, BM=32, seed=21):
     return c, g, q, s, sorted_ids, eids, ntpp
 
 
+@pytest.mark.parametrize("tiles", sorted(SETUPS))
 @pytest.mark.parametrize("chunks", [[128, 256, 384], [384, 384], [768]])
-def test_n_split_assembles_the_full_gemm(chunks):
+def test_n_split_assembles_the_full_gemm(chunks, tiles):
     import torch
 
     from td_benchmark_amd import ops
 
-    print(f"case: n_split {chunks}", flush=True)
-    c, g, q, s, sorted_ids, eids, ntpp = _setup()
+    print(f"case: n_split {chunks} {tiles}", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup(**SETUPS[tiles])
     N = 2 * c.I
     assert sum(chunks) == N
     full = torch.zeros((c.S, N), dtype=torch.bfloat16, device="cuda")
@@ -77,14 +82,15 @@ def test_n_split_w2_routed_rows_by_position():
     assert np.array_equal(bf16_bits(parts), bf16_bits(full))
 
 
+@pytest.mark.parametrize("tiles", sorted(SETUPS))
 @pytest.mark.parametrize("bounds", [[0, 256, 512], [0, 128, 384, 512], [0, 512]])
-def test_k_split_accumulates_like_the_reference(bounds):
+def test_k_split_accumulates_like_the_reference(bounds, tiles):
     import torch
 
     from td_benchmark_amd import ops
 
-    print(f"case: k_split {bounds}", flush=True)
-    c, g, q, s, sorted_ids, eids, ntpp = _setup()
+    print(f"case: k_split {bounds} {tiles}", flush=True)
+    c, g, q, s, sorted_ids, eids, ntpp = _setup(**SETUPS[tiles])
     eids_masked = eids.clone()
     eids_masked[1] = -1                      # a non-local block: zeros on the first chunk only
     N = 2 * c.I

@@ -198,6 +198,7 @@ GEMM_CASES = [
     (128, 2048, 256, 64, 8, 16, "zipf"),
     (600, 512, 384, 4, 2, 256, "softmax"),   # align blocks of 256 rows
     (700, 256, 256, 4, 2, 64, "zipf"),       # S >= 160*E: 256-row tiles over 64-row blocks
+    (700, 384, 256, 4, 2, 64, "softmax"),    # 256-row tiles, W2 with an odd count of 128-column groups
 ]
 
 
