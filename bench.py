@@ -30,7 +30,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "FP8 grouped-GEMM TFLOP/s (% MFMA peak) + MoE layer µs, DeepSeek-V3 shape, 1 GPU"
 PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
-STAGES = ("quant", "align", "w13", "w2", "reduce")
+STAGES = ("quant", "align", "scales", "w13", "w2", "reduce")
 
 
 def stage_bytes(wl, ntpp: int, active: int, BM: int | None = None) -> dict[str, float]:
@@ -43,6 +43,8 @@ def stage_bytes(wl, ntpp: int, active: int, BM: int | None = None) -> dict[str, 
     return {
         "quant": 2 * T * H + T * H + 4 * T * H / 128,
         "align": 4 * S + 4 * ntpp + 4 * ntpp / BM + 4,
+        # activation scales by sorted position: ids read, one scale row read and written per slot
+        "scales": 4 * ntpp + 8 * S * H / 128,
         "w13": w13 + T * H + 4 * T * H / 128 + S * I + 4 * S * I / 128,
         "w2": w2 + S * I + 4 * S * I / 128 + 2 * S * H + 4 * S,
         "reduce": 2 * S * H + 2 * T * H,
@@ -184,20 +186,23 @@ def main() -> int:
         runner.stage_align(data.topk_ids)
         if ev is not None:
             ev[2].record()
-        runner.stage_w13()
+        runner.stage_scales()
         if ev is not None:
             ev[3].record()
-        runner.stage_w2(data.topk_w)
+        runner.stage_w13()
         if ev is not None:
             ev[4].record()
-        runner.stage_reduce()
+        runner.stage_w2(data.topk_w)
         if ev is not None:
             ev[5].record()
+        runner.stage_reduce()
+        if ev is not None:
+            ev[6].record()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()

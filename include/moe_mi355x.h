@@ -172,6 +172,41 @@ int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const vo
                                   int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
                                   int64_t max_padded, int32_t tile_m, void* hq, float* hs, void* stream);
 
+/* Scales by sorted position (no counterpart in the reference: a layout between
+ * the build's own kernels, for the prebuilt layer).  The GEMMs above read a
+ * tile's activation scales for one K block as one scale per row, each from a
+ * different row of A_scale; these variants take them K-major by sorted
+ * position, so the tile's scales of one K block are contiguous.  Results are
+ * bit-identical to the variants above.
+ *
+ * moe_gather_scales_by_position: out [groups, max_padded] fp32,
+ *   out[kb, p] = scales[sorted_ids[p] / top_k, kb] for p < *ntpp holding a
+ *   slot (< S), and scales[0, kb] for padding positions and p >= *ntpp (the
+ *   row the row-major GEMMs read for a padding position, so the outputs at
+ *   padding positions agree too).  scales [rows, groups] with rows >=
+ *   ceil(S / top_k) (the 1x128 quant's scales). */
+int moe_gather_scales_by_position(const float* scales, int64_t rows, int64_t groups,
+                                  const int32_t* sorted_ids, const int32_t* ntpp, int64_t S, int32_t top_k,
+                                  int64_t max_padded, float* out, void* stream);
+
+/* The fused W13 with A_scale_pos [H/128, max_padded] (gathered as above) and
+ * its output scales hs_pos [I/128, max_padded] K-major by sorted position
+ * (hq as for moe_gemm_w13_silu_quant). */
+int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_pos, const void* W13,
+                                const float* W13_scale, const int32_t* sorted_ids,
+                                const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
+                                int64_t max_padded, int32_t tile_m, void* hq, float* hs_pos, void* stream);
+
+/* The W2 GEMM (A rows by sorted position, as a_by_pos = 1, C rows by slot,
+ * routed weights if topk_weights is not null) with A_scale_pos [K/128,
+ * max_padded] K-major by sorted position, as moe_gemm_w13_silu_quant_pos
+ * writes it. */
+int moe_grouped_gemm_pos(const void* A, const float* A_scale_pos, const void* B, const float* B_scale,
+                         const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                         const float* topk_weights, int64_t S, int64_t N, int64_t K, int32_t E,
+                         int32_t block_size_m, int64_t max_padded, int32_t tile_m, void* C, void* stream);
+
 /* A6 -- silu_and_mul.  Replaces torch.ops._C.silu_and_mul(out, in)
  * (overlap/overlap_forward.py:277-279): h[r,j] = bf16(silu(c[r,j]) * c[r,I+j]).
  * c [R, 2I] bf16 -> h [R, I] bf16; I % 8 == 0. */

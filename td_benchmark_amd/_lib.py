@@ -53,6 +53,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "moe_silu_mul_quant_group128": (ctypes.c_int, [_P, _i64, _i64, _P, _P, _P]),
     "moe_reduce_topk_add": (ctypes.c_int, [_P, _P, _i64, _i32, _i64, _P, _P]),
     "moe_fp8_dequant_sum": (ctypes.c_int, [_P, _P, _i64, _i64, _i64, _i64, _P, _i64, _P]),
+    "moe_gather_scales_by_position": (ctypes.c_int, [_P, _i64, _i64, _P, _P, _i64, _i32, _i64, _P, _P]),
+    "moe_gemm_w13_silu_quant_pos": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64, _i64, _i32, _i32,
+                                                   _i64, _i32, _P, _P, _P]),
+    "moe_grouped_gemm_pos": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i64, _i64, _i32, _i32, _i64, _i32,
+                                            _P, _P]),
     "moe_gemm_w13_silu_quant": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
                                                _i64, _i32, _i32, _i64, _P, _P, _P]),
     "moe_gemm_w13_silu_quant_tiled": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,

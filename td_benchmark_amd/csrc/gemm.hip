@@ -148,7 +148,17 @@ struct GemmArgs {
   int64_t bs_es;           // B_scale expert stride, floats
   int64_t ldc;             // C row stride, elements (plain epilogue)
   int accumulate;          // plain epilogue: C = bf16(C + bf16(result)) instead of C = bf16(result)
+  // Activation scales K-major by sorted position, As[kb * as_pos_ld + pos] (0: As[a_row * as_ld + kb]).
+  // Each K step's scales of a tile are then one contiguous run of its rows.
+  int64_t as_pos_ld;
+  // Fused epilogue: hs K-major, hs[j * hs_pos_ld + pos] (0: hs[pos * I/128 + j]).
+  int64_t hs_pos_ld;
 };
+
+// Element (position pos, group j) of the fused epilogue's scale output.
+MOE_DEVICE float* hs_at(const GemmArgs& g, int64_t pos, int64_t j) {
+  return g.hs_pos_ld ? g.hs + j * g.hs_pos_ld + pos : g.hs + pos * (g.I / 128) + j;
+}
 
 // Dense (unsliced) strides for A [rows, K], B [E, N, K], C [S, N].
 static inline void dense_strides(GemmArgs& g) {
@@ -262,7 +272,6 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
       }
     __syncthreads();
     uint8_t* stage_out = staging;  // [BM][128] fp8 codes
-    const int64_t hgroups = g.I / 128;
 #pragma unroll
     for (int r = 0; r < T::RS; ++r)
 #pragma unroll
@@ -273,7 +282,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
         for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
         const float sc = group_scale(amax);
         const float inv = 1.0f / sc;
-        if (wn == 0 && fr == 0 && row < rows_avail) g.hs[(pos0 + row) * hgroups + j] = sc;
+        if (wn == 0 && fr == 0 && row < rows_avail) *hs_at(g, pos0 + row, j) = sc;
 #pragma unroll
         for (int c = 0; c < T::CS; c += 2) {
           const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
@@ -399,7 +408,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   uint32_t sa_off = 0;
   if (s_idx < T::NS) {
     const int row = 64 * s_idx + lane;
-    sa_off = (uint32_t)(a_row_of(row < BM ? row : 0) * g.as_ld) * 4u;
+    // by position, rows past the run read the tile's first row (their outputs are not stored)
+    sa_off = g.as_pos_ld ? (uint32_t)(pos0 + (row < rows_avail ? row : 0)) * 4u
+                         : (uint32_t)(a_row_of(row < BM ? row : 0) * g.as_ld) * 4u;
   }
   int64_t g0, g1;
   bool g1_store;
@@ -439,7 +450,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     if (s_idx < T::NS) {
       uint32_t soff = sa_off;
       asm volatile("" : "+v"(soff));
-      dma4(reinterpret_cast<const uint8_t*>(g.As + kk) + soff,
+      dma4(reinterpret_cast<const uint8_t*>(g.as_pos_ld ? g.As + kk * g.as_pos_ld : g.As + kk) + soff,
            smem + T::OFF_SA + stage * T::NS * 256 + s_idx * 256);
     }
   };
@@ -714,7 +725,7 @@ void grouped_gemm_kernel(GemmArgs g) {
         *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
       }
       for (int row = tid; row < rows_avail; row += T::THREADS)
-        g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
+        *hs_at(g, pos0 + row, j) = kScaleFloor;
     } else {
       for (int ci = tid; ci < rows_avail * 32; ci += T::THREADS) {
         const int row = ci >> 5, cc = ci & 31;
@@ -747,7 +758,7 @@ void grouped_gemm_kernel(GemmArgs g) {
           *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
         }
         for (int row = kTailRows + tid; row < rows_avail; row += T::THREADS)
-          g.hs[(pos0 + row) * (g.I / 128) + j] = kScaleFloor;
+          *hs_at(g, pos0 + row, j) = kScaleFloor;
       }
       return;
     }
@@ -806,13 +817,13 @@ static bool offsets_fit(int64_t rows, int64_t N, int64_t K) {
 
 using namespace moe;
 
-extern "C" int moe_grouped_gemm_tiled(const void* A, const float* A_scale, const void* B,
-                                      const float* B_scale, const int32_t* sorted_ids,
-                                      const int32_t* expert_ids, const int32_t* ntpp,
-                                      const float* topk_weights, int64_t S, int32_t top_k,
-                                      int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
-                                      int64_t max_padded, int32_t tile_order, int32_t tile_m,
-                                      void* C, void* stream) {
+// The plain grouped GEMM on dense operands; A_scale row-major by A row, or
+// K-major by sorted position when scales_by_pos (A then by position too).
+static int plain_gemm(const void* A, const float* A_scale, const void* B, const float* B_scale,
+                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                      const float* topk_weights, int64_t S, int32_t top_k, int32_t a_by_pos, int64_t N,
+                      int64_t K, int32_t E, int32_t BM, int64_t max_padded, int32_t tile_order,
+                      int32_t tile_m, bool scales_by_pos, void* C, void* stream) {
   if (S < 0 || N <= 0 || K <= 0 || max_padded < 0) return kErrBadShape;
   if (N % 128 != 0 || K % 128 != 0 || K > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
@@ -849,7 +860,28 @@ extern "C" int moe_grouped_gemm_tiled(const void* A, const float* A_scale, const
   g.E = E;
   g.tile_order = tile_order;
   dense_strides(g);
+  if (scales_by_pos) g.as_pos_ld = max_padded;
   return dispatch_gemm<false>(TM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_grouped_gemm_tiled(const void* A, const float* A_scale, const void* B,
+                                      const float* B_scale, const int32_t* sorted_ids,
+                                      const int32_t* expert_ids, const int32_t* ntpp,
+                                      const float* topk_weights, int64_t S, int32_t top_k,
+                                      int32_t a_by_pos, int64_t N, int64_t K, int32_t E, int32_t BM,
+                                      int64_t max_padded, int32_t tile_order, int32_t tile_m,
+                                      void* C, void* stream) {
+  return plain_gemm(A, A_scale, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, top_k, a_by_pos, N, K,
+                    E, BM, max_padded, tile_order, tile_m, false, C, stream);
+}
+
+extern "C" int moe_grouped_gemm_pos(const void* A, const float* A_scale_pos, const void* B,
+                                    const float* B_scale, const int32_t* sorted_ids,
+                                    const int32_t* expert_ids, const int32_t* ntpp,
+                                    const float* topk_weights, int64_t S, int64_t N, int64_t K, int32_t E,
+                                    int32_t BM, int64_t max_padded, int32_t tile_m, void* C, void* stream) {
+  return plain_gemm(A, A_scale_pos, B, B_scale, sorted_ids, expert_ids, ntpp, topk_weights, S, 1, 1, N, K, E, BM,
+                    max_padded, 0, tile_m, true, C, stream);
 }
 
 extern "C" int moe_grouped_gemm_ordered(const void* A, const float* A_scale, const void* B,
@@ -976,12 +1008,12 @@ extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int
   return dispatch_gemm<false>(TM, g, (hipStream_t)stream);
 }
 
-extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const void* W13,
-                                             const float* W13_scale, const int32_t* sorted_ids,
-                                             const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
-                                             int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM,
-                                             int64_t max_padded, int32_t tile_m, void* hq, float* hs,
-                                             void* stream) {
+// The fused W13 GEMM; scales row-major (A_scale by token, hs by position), or
+// both K-major by sorted position when scales_by_pos.
+static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const float* W13_scale,
+                    const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                    int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM, int64_t max_padded,
+                    int32_t tile_m, bool scales_by_pos, void* hq, float* hs, void* stream) {
   if (S < 0 || H <= 0 || I <= 0 || max_padded < 0) return kErrBadShape;
   if (H % 128 != 0 || I % 128 != 0 || H > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
@@ -1016,7 +1048,84 @@ extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scal
   g.a_by_pos = 0;
   g.E = E;
   dense_strides(g);
+  if (scales_by_pos) g.as_pos_ld = g.hs_pos_ld = max_padded;
   return dispatch_gemm<true>(TM, g, (hipStream_t)stream);
+}
+
+extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const void* W13,
+                                             const float* W13_scale, const int32_t* sorted_ids,
+                                             const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                             int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM,
+                                             int64_t max_padded, int32_t tile_m, void* hq, float* hs,
+                                             void* stream) {
+  return w13_gemm(Aq, A_scale, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k, H, I, E, BM, max_padded,
+                  tile_m, false, hq, hs, stream);
+}
+
+extern "C" int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_pos, const void* W13,
+                                           const float* W13_scale, const int32_t* sorted_ids,
+                                           const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                           int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM,
+                                           int64_t max_padded, int32_t tile_m, void* hq, float* hs_pos,
+                                           void* stream) {
+  return w13_gemm(Aq, A_scale_pos, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k, H, I, E, BM, max_padded,
+                  tile_m, true, hq, hs_pos, stream);
+}
+
+namespace moe {
+
+// out[kb * max_padded + p] = scales[row(p) * groups + kb], row(p) =
+// sorted[p] / top_k for the positions p < ntpp that hold a slot and row 0
+// otherwise -- the A row the row-major path reads for a padding position, so
+// both layouts give the same outputs at every position.
+// One thread per (position, 4 K blocks), positions fastest, so each K block's
+// row of out is written coalesced and every thread has one load in flight.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void gather_scales_kernel(const float* __restrict__ scales, int64_t groups,
+                                                            const int32_t* __restrict__ sorted,
+                                                            const int32_t* __restrict__ ntpp, int64_t S,
+                                                            int top_k, int64_t max_padded,
+                                                            float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t chunks = (groups + 3) / 4;
+  if (idx >= max_padded * chunks) return;
+  const int64_t c = idx / max_padded, p = idx % max_padded;
+  int64_t row = 0;
+  if (p < *ntpp) {
+    const int32_t slot = sorted[p];
+    if (slot < S) row = slot / top_k;
+  }
+  const int64_t kb0 = 4 * c;
+  const float* src = scales + row * groups + kb0;
+  if constexpr (VEC4) {
+    const v4f v = *reinterpret_cast<const v4f*>(src);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[(kb0 + q) * max_padded + p] = v[q];
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb0 + q < groups) out[(kb0 + q) * max_padded + p] = src[q];
+  }
+}
+
+}  // namespace moe
+
+extern "C" int moe_gather_scales_by_position(const float* scales, int64_t rows, int64_t groups,
+                                             const int32_t* sorted_ids, const int32_t* ntpp, int64_t S,
+                                             int32_t top_k, int64_t max_padded, float* out, void* stream) {
+  if (rows < 0 || groups <= 0 || S < 0 || max_padded < 0) return kErrBadShape;
+  if (top_k <= 0) return kErrBadTopK;
+  if (max_padded == 0) return kOk;
+  if (!scales || !sorted_ids || !ntpp || !out) return kErrNullPointer;
+  if (rows < (S + top_k - 1) / top_k) return kErrCapacity;
+  const unsigned blocks = (unsigned)((max_padded * ((groups + 3) / 4) + 255) / 256);
+  if (groups % 4 == 0 && ((uintptr_t)scales & 15) == 0)
+    hipLaunchKernelGGL(gather_scales_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, scales, groups,
+                       sorted_ids, ntpp, S, (int)top_k, max_padded, out);
+  else
+    hipLaunchKernelGGL(gather_scales_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, scales, groups,
+                       sorted_ids, ntpp, S, (int)top_k, max_padded, out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, const void* W13,

@@ -381,6 +381,33 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
     return hq, hs
 
 
+def gather_scales_by_position(scales: torch.Tensor, sorted_token_ids: torch.Tensor,
+                              num_tokens_post_padded: torch.Tensor, num_slots: int, top_k: int,
+                              out: torch.Tensor | None = None) -> torch.Tensor:
+    """1x128 activation scales [rows, G] (by token) -> [G, max_padded] K-major by
+    sorted position: out[kb, p] = scales[sorted_token_ids[p] // top_k, kb] for the
+    positions that hold a slot and scales[0, kb] elsewhere (the row the
+    row-major GEMMs read for a padding position).  The layout the position-major
+    GEMMs of FusedExpertsRunner read (contiguous per K block and tile); it has
+    no counterpart in the reference."""
+    if scales.dim() != 2:
+        raise ValueError(f"scales must be [rows, groups], got {tuple(scales.shape)}")
+    if top_k < 1:
+        raise ValueError("top_k must be >= 1")
+    _need(scales, "scales", torch.float32)
+    _need(sorted_token_ids, "sorted_token_ids", torch.int32)
+    _need(num_tokens_post_padded, "num_tokens_post_padded", torch.int32)
+    rows, G = scales.shape
+    mp = sorted_token_ids.numel()
+    if out is None:
+        out = torch.empty((G, mp), dtype=torch.float32, device=scales.device)
+    _need(out, "out", torch.float32, (G, mp))
+    check(lib().moe_gather_scales_by_position(_ptr(scales), rows, G, _ptr(sorted_token_ids),
+                                              _ptr(num_tokens_post_padded), num_slots, top_k, mp, _ptr(out),
+                                              _stream()), "moe_gather_scales_by_position")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # A6 / A9
 # ---------------------------------------------------------------------------
@@ -594,13 +621,24 @@ class FusedExpertsRunner:
     Construction allocates every buffer; ``run`` only enqueues kernels
     (quant -> align -> W13+SiLU+quant -> W2 with routed weights ->
     [shared expert on the same FP8 input] -> top-k sum) on the current stream
-    and returns the [T, H] bf16 output (``out`` if one was given)."""
+    and returns the [T, H] bf16 output (``out`` if one was given).
+
+    With ``scales_by_position`` (by default when the GEMM tiles have 128 or
+    more rows, where a step's scales are worth a contiguous load) the
+    activation scales travel K-major by sorted position between the kernels: the W13 stage first
+    gathers the 1x128 scales into that layout, and the fused W13 writes its
+    output scales in it for W2, so each GEMM step reads its tile's scales as
+    one contiguous run.  Results are bit-identical to the row-major path.
+    ``hs`` is then a [max_padded, I/128] view of the K-major buffer.  Run one
+    stage at a time with ``stage_quant``, ``stage_align``, ``stage_scales``,
+    ``stage_w13``, ``stage_w2``, ``stage_shared``, ``stage_reduce``, in that
+    order."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
                  shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None,
                  global_num_experts: int | None = None, expert_map: torch.Tensor | None = None,
-                 tile_m: int = 0):
+                 tile_m: int = 0, scales_by_position: bool | None = None):
         E, N2, H = _need_weights(w13, w13_scale, "w13")
         _need_weights(w2, w2_scale, "w2")
         if w2.shape != (E, H, N2 // 2):
@@ -636,7 +674,15 @@ class FusedExpertsRunner:
         self.align = AlignBuffers(self.S, n_align, self.BM, dev)
         mp = max(self.align.max_padded, 1)
         self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
-        self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
+        if scales_by_position is None:
+            scales_by_position = gemm_tile_rows(self.BM, self.S, self.E, self.tile_m) >= 128
+        self.scales_by_position = bool(scales_by_position)
+        if self.scales_by_position:
+            self.s1_pos = torch.empty((H // 128, mp), dtype=torch.float32, device=dev)
+            self.hs_pos = torch.empty((self.I // 128, mp), dtype=torch.float32, device=dev)
+            self.hs = self.hs_pos.t()  # [mp, I/128] view by position
+        else:
+            self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
         self.D = torch.empty((max(self.S, 1), H), dtype=torch.bfloat16, device=dev)
         if out is not None:
             _need(out, "out", torch.bfloat16)
@@ -654,8 +700,24 @@ class FusedExpertsRunner:
     def stage_align(self, topk_ids: torch.Tensor) -> None:
         self.align.run(topk_ids, self.expert_map)
 
+    def stage_scales(self) -> None:
+        """The activation scales K-major by sorted position for the W13 GEMM
+        (nothing to do on the row-major path)."""
+        if self.scales_by_position:
+            a = self.align
+            check(lib().moe_gather_scales_by_position(_ptr(self.s1), self.T, self.H // 128, _ptr(a.sorted_ids),
+                                                      _ptr(a.ntpp), self.S, self.top_k, a.max_padded,
+                                                      _ptr(self.s1_pos), _stream()), "moe_gather_scales_by_position")
+
     def stage_w13(self) -> None:
         a = self.align
+        if self.scales_by_position:
+            check(lib().moe_gemm_w13_silu_quant_pos(_ptr(self.q1), _ptr(self.s1_pos), _ptr(self.w13),
+                                                    _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
+                                                    _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
+                                                    self.BM, a.max_padded, self.tile_m, _ptr(self.hq),
+                                                    _ptr(self.hs_pos), _stream()), "moe_gemm_w13_silu_quant_pos")
+            return
         check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(self.q1), _ptr(self.s1), _ptr(self.w13),
                                                   _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
                                                   _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
@@ -667,6 +729,13 @@ class FusedExpertsRunner:
         if topk_weights.numel() != self.S:
             raise ValueError(f"topk_weights has {topk_weights.numel()} entries for {self.S} slots")
         a = self.align
+        if self.scales_by_position:
+            check(lib().moe_grouped_gemm_pos(_ptr(self.hq), _ptr(self.hs_pos), _ptr(self.w2), _ptr(self.w2_scale),
+                                             _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
+                                             _ptr(topk_weights), self.S, self.H, self.I, self.E, self.BM,
+                                             a.max_padded, self.tile_m, _ptr(self.D), _stream()),
+                  "moe_grouped_gemm_pos")
+            return
         check(lib().moe_grouped_gemm_tiled(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
                                            _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
                                            _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
@@ -685,6 +754,7 @@ class FusedExpertsRunner:
     def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
         self.stage_quant(hidden)
         self.stage_align(topk_ids)
+        self.stage_scales()
         self.stage_w13()
         self.stage_w2(topk_weights)
         self.stage_shared()

@@ -110,7 +110,7 @@ SPEC = SchemeSpec(
     },
 )
 
-_STAGES = ("quant", "align", "w13", "w2", "shared", "reduce")
+_STAGES = ("quant", "align", "scales", "w13", "w2", "shared", "reduce")
 
 
 def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
@@ -173,15 +173,17 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
         ev[1].record()
         runner.stage_align(ids)
         ev[2].record()
-        runner.stage_w13()
+        runner.stage_scales()
         ev[3].record()
-        runner.stage_w2(wts)
+        runner.stage_w13()
         ev[4].record()
-        runner.stage_shared()
+        runner.stage_w2(wts)
         ev[5].record()
-        runner.stage_reduce()
+        runner.stage_shared()
         ev[6].record()
-        ev[6].synchronize()
+        runner.stage_reduce()
+        ev[7].record()
+        ev[7].synchronize()
         return StageResult(output=runner.y,
                            stage_ms={n: ev[i].elapsed_time(ev[i + 1]) for i, n in enumerate(_STAGES)})
 

@@ -195,7 +195,7 @@ def test_scheme_m1_run_meets_golden_gates(tunables):
     staged = inst.run_staged()
     assert np.array_equal(bf16_bits(staged.output), bf16_bits(y))
     if not tunables.get("n_chunks"):
-        assert set(staged.stage_ms) == {"quant", "align", "w13", "w2", "shared", "reduce"}
+        assert set(staged.stage_ms) == {"quant", "align", "scales", "w13", "w2", "shared", "reduce"}
     assert inst.diagnostics["scheme"] == "m1" and inst.diagnostics["shared_expert"] is True
     inst.close()
     with pytest.raises(RuntimeError, match="closed"):
