@@ -40,10 +40,12 @@
 // only step k+1's loads are in flight, passes one barrier, issues step k+2's
 // loads into the buffer freed at step k-1, then computes.  TM = 16 and 32 (the
 // weight-streaming decode tiles) keep a 4-stage ring, two younger stages in
-// flight.  At TM = 256 three 64 KiB
-// stages exceed the LDS, so the ring has two stages and every step waits for
-// all of its loads; A rows of subtiles without a valid row are then not
-// fetched.
+// flight.  At TM = 256 three 64 KiB stages exceed the LDS, so the ring has two
+// stages and every step waits for all of its loads; A rows of subtiles without
+// a valid row are then not fetched.  The activation scales of a stage are one
+// 4-byte direct-to-LDS load per row: from the row's own scale row, or -- when
+// they are laid out K-major by sorted position (as_pos_ld) -- one contiguous
+// run of the tile's rows per K block.
 //
 // LDS rows are 128 B; the 16 B chunk index of a row is XORed with
 // swz(row) = (row mod 8) ^ bit3(row), which depends only on the row's
