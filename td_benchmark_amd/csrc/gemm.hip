@@ -226,7 +226,7 @@ MOE_DEVICE void groups_of(const GemmArgs& g, int64_t j, int64_t& g0, int64_t& g1
 
 // The epilogue of one tile, shared by both K-loop bodies: SiLU*up and the
 // 1x128 quant of h written by sorted position (fused W13), or the bf16 rows
-// (routed weights applied) written by slot.  `staging` is LDS for BM x 256 B.
+// (routed weights applied) written by slot.  `staging` is LDS for BM x 512 B.
 // Output element (r, gg, c, v) of a lane: row = row_base + r*16 + 4*kseg + v,
 // column (within group gg) = col_base + c*16 + fr.
 template <int BM, bool FUSED>
@@ -301,45 +301,45 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
           *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
     }
   } else {
-    // One 128-column group per pass, staged as [BM][128] bf16.
+    // Both 128-column groups staged at once as [BM][256] bf16, then each row's
+    // chunks (up to 512 B) written by slot.
     uint16_t* stage_out = reinterpret_cast<uint16_t*>(staging);
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      if (gg == 1 && !g1_store) break;
-      if (gg == 1) __syncthreads();  // the first pass's stores have read the staging
+    for (int r = 0; r < T::RS; ++r)
 #pragma unroll
-      for (int r = 0; r < T::RS; ++r)
+      for (int v = 0; v < 4; ++v) {
+        const int row = row_base + r * 16 + 4 * kseg + v;
+        const float w = smW[row];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = row_base + r * 16 + 4 * kseg + v;
-          const float w = smW[row];
+        for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
           for (int c = 0; c < T::CS; ++c) {
             float val = acc[r][gg][c][v];
             if (g.topk_w) val = val * w;
-            stage_out[row * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
+            stage_out[row * 256 + gg * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
           }
-        }
-      __syncthreads();
-      const int64_t n0 = (gg ? g1 : g0) * 128;
-      for (int ci = tid; ci < BM * 16; ci += T::THREADS) {
-        const int row = ci >> 4, cc = ci & 15;
-        const int64_t slot = smSlot[row];
-        if (slot >= g.S) continue;
-        v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 8);
-        v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n0 + cc * 8);
-        if (g.accumulate) {
-          // K-split accumulation: the bf16 partial is added to the bf16 C of the
-          // earlier chunks and rounded again.
-          const v4i old = *dst;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
-            val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
-          }
-        }
-        *dst = val;
       }
+    __syncthreads();
+    const int nchunks = g1_store ? 32 : 16;  // 16 B chunks of a row to store
+    for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
+      const int row = ci >> 5, cc = ci & 31;
+      if (cc >= nchunks) continue;
+      const int64_t slot = smSlot[row];
+      if (slot >= g.S) continue;
+      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
+      const int64_t n = (cc < 16 ? g0 : g1) * 128 + (cc & 15) * 8;
+      v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
+      if (g.accumulate) {
+        // K-split accumulation: the bf16 partial is added to the bf16 C of the
+        // earlier chunks and rounded again.
+        const v4i old = *dst;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
+          val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
+        }
+      }
+      *dst = val;
     }
   }
 }
@@ -495,7 +495,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 #pragma unroll
       for (int c = 0; c < T::CS; ++c) acc[r][gg][c] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 
-  int stage_last = 0;
   auto kloop = [&](auto ra_c) {
     constexpr int RA = decltype(ra_c)::value;  // active 16-row subtiles of this wave
     int stage = 0;
@@ -594,7 +593,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
               ...);
         }(std::make_integer_sequence<int, LG>{});
       }
-      stage_last = stage;
       stage = (stage == T::KS - 1) ? 0 : stage + 1;
     }
   };
@@ -605,11 +603,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     case 3: if constexpr (T::RS >= 3) kloop(std::integral_constant<int, (T::RS >= 3 ? 3 : 0)>{}); break;
     default: if constexpr (T::RS >= 4) kloop(std::integral_constant<int, (T::RS >= 4 ? 4 : 0)>{}); break;
   }
-  block_barrier();  // every wave is done with the last step's buffer; stage the output there
-
-  static_assert(BM * 256 <= T::STAGE, "one group's bf16 output must fit in a stage");
-  tile_epilogue<BM, FUSED>(g, acc, j, pos0, rows_avail, g0, g1, g1_store, smem + stage_last * T::STAGE, smRed,
-                           smSlot, smW);
+  // Every wave is done with the operand ring (the last step waited for all of
+  // its loads); the epilogue stages the output at its base.
+  block_barrier();
+  tile_epilogue<BM, FUSED>(g, acc, j, pos0, rows_avail, g0, g1, g1_store, smem, smRed, smSlot, smW);
 
 }
 
