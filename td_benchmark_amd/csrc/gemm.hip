@@ -700,7 +700,7 @@ void grouped_gemm_kernel(GemmArgs g) {
   // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
   // the GG workgroups that share an A tile start together and reuse it from
   // L2, and a weight tile is still read by all row tiles of the run close in time.
-  constexpr int64_t GG = FUSED ? 8 : 4;
+  constexpr int64_t GG = 4;  // 2, 8 and 16 (W13), 2, 3, 7 and 14 (W2) measured slower
   const int64_t gj0 = in_run / (GG * units) * GG;
   const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
   const int64_t in_grp = in_run - gj0 * units;
