@@ -518,7 +518,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         [&]<int... R>(std::integer_sequence<int, R...>) {
           ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
         }(std::make_integer_sequence<int, RA>{});
-        // Column fragments double-buffered; MFMA t is issued before the scale
+        // Column fragments triple-buffered (two LDS reads in flight ahead of the
+        // MFMAs that use them); MFMA t is issued before the scale
         // FMAs of MFMA t-kScaleLag, whose result is ready by then.  The per-row
         // scale products a_s*b_s are formed per group; the MFMAs of the first
         // group still pending at the group switch (its last kScaleLag, rows
@@ -526,11 +527,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         constexpr int LG = kScaleLag;
         constexpr int NQ = 2 * T::CS;  // column fragments per step
         constexpr int NT = NQ * RA;
-        v8i bq[2];
+        constexpr int NBQ = 3;
+        v8i bq[NBQ];
         v4f p[LG + 1];
         float sab[RA][4];
         float sab_prev[LG][4];
         bq[0] = frag_at<0>(pb0, pb1);
+        if constexpr (NQ > 1) bq[1] = frag_at<(1 / T::CS * 128 + 1 % T::CS * 16) * 128>(pb0, pb1);
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
           (
               [&] {
@@ -550,14 +553,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
                     for (int v = 0; v < 4; ++v) sab[r][v] = sa4[v] * sb;
                   }
                 }
-                if constexpr (Q + 1 < NQ) {
-                  constexpr int gn = (Q + 1) / T::CS, cn = (Q + 1) % T::CS;
-                  bq[(Q + 1) & 1] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
+                if constexpr (Q + NBQ - 1 < NQ) {
+                  constexpr int gn = (Q + NBQ - 1) / T::CS, cn = (Q + NBQ - 1) % T::CS;
+                  bq[(Q + NBQ - 1) % NBQ] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
                 }
 #pragma unroll
                 for (int r = 0; r < RA; ++r) {
                   const int t = Q * RA + r;
-                  p[t % (LG + 1)] = mfma_fp8(af[r], bq[Q & 1]);
+                  p[t % (LG + 1)] = mfma_fp8(af[r], bq[Q % NBQ]);
                   if (t >= LG) {
                     const int u = t - LG, uq = u / RA, ur = u % RA;
                     const int ug = uq / T::CS, uc = uq % T::CS;
