@@ -57,9 +57,10 @@ def test_bench_stage_bytes_and_traffic_lookup():
     # W13 weights dominate: 256 experts x 2I x H bytes
     assert b["w13"] > 256 * 2 * 2048 * 7168
     assert b["reduce"] == 2 * wl.S * wl.H + 2 * wl.T * wl.H
-    traffic, src = bench.measured_traffic("dsv3", "grouped_gemm_kernel<128,true>")
-    if src is not None:
-        assert traffic > b["w13"] * 0.5
+    # the committed PMC summary holds the W13 launch's traffic at DSv3 (256-row tiles)
+    traffic, src = bench.measured_traffic("dsv3", "grouped_gemm_kernel<256,true>")
+    assert src == "moe_layer_dsv3_hbm_traffic.md"
+    assert b["w13"] < traffic < 1.5 * b["w13"]
     assert bench.measured_traffic("no_such_workload", "x") == (None, None)
 
 
