@@ -619,8 +619,9 @@ class FusedExpertsRunner:
     """Prebuilt A1->A9 chain for fixed (T, H, I, E, top_k, BM).
 
     Construction allocates every buffer; ``run`` only enqueues kernels
-    (quant -> align -> W13+SiLU+quant -> W2 with routed weights ->
-    [shared expert on the same FP8 input] -> top-k sum) on the current stream
+    (quant -> align -> [scale gather] -> W13+SiLU+quant -> W2 with routed
+    weights -> [shared expert on the same FP8 input] -> top-k sum) on the
+    current stream
     and returns the [T, H] bf16 output (``out`` if one was given).
 
     With ``scales_by_position`` (by default when the GEMM tiles have 128 or
