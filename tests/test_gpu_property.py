@@ -76,3 +76,33 @@ def test_gpu_quant_matches_oracle_on_random_bits(bits):
     rq, rs = oracle.quant_group128(bits)
     assert np.array_equal(u8_bits(q), rq)
     assert np.array_equal(s.cpu().numpy(), rs)
+
+
+@st.composite
+def expert_rows(draw):
+    T = draw(st.integers(1, 40))
+    k = draw(st.integers(1, 32))
+    H = 8 * draw(st.integers(1, 64))
+    seed = draw(st.integers(0, 2**31 - 1))
+    rng = np.random.default_rng(seed)
+    bits = rng.integers(0, 0x10000, size=(T * k + T, H), dtype=np.uint32).astype(np.uint16)
+    exp = (bits >> 7) & 0xFF
+    bits = np.where(exp > 0xE3, (bits & 0x807F) | (0xE3 << 7), bits).astype(np.uint16)  # |v| < 2^101: no overflow
+    return bits[: T * k], bits[T * k :], T, k, draw(st.booleans())
+
+
+@settings(max_examples=60, deadline=None, derandomize=True)
+@given(expert_rows())
+def test_gpu_reduce_matches_oracle_on_random_rows(case):
+    """moe_sum (overlap_forward.py:304-313), with and without the shared
+    expert's addend (schemes/vllm_tp.py:62-63): bit-exact with the oracle."""
+    from td_benchmark_amd import ops
+    D, add, T, k, with_add = case
+    dev = lambda b: torch.from_numpy(b.view(np.int16)).cuda().view(torch.bfloat16)  # noqa: E731
+    y = torch.empty((T, D.shape[1]), dtype=torch.bfloat16, device="cuda")
+    ops.moe_sum(dev(D), y, k, addend=dev(add) if with_add else None)
+    torch.cuda.synchronize()
+    want = oracle.moe_reduce(D, T, k)
+    if with_add:
+        want = oracle.f32_to_bf16(oracle.bf16_to_f32(want) + oracle.bf16_to_f32(add))
+    assert np.array_equal(u8_bits(y).view(np.uint16), want)
