@@ -106,3 +106,32 @@ def test_gpu_reduce_matches_oracle_on_random_rows(case):
     if with_add:
         want = oracle.f32_to_bf16(oracle.bf16_to_f32(want) + oracle.bf16_to_f32(add))
     assert np.array_equal(u8_bits(y).view(np.uint16), want)
+
+
+@st.composite
+def rs_chunks(draw):
+    R = draw(st.integers(1, 64))
+    M = draw(st.integers(1, 24))
+    N = 16 * draw(st.integers(1, 40))
+    G = (N + 127) // 128 + draw(st.integers(0, 2))        # scale rows may be wider
+    ld = N + 8 * draw(st.integers(0, 4))                    # a column slice of a wider output
+    seed = draw(st.integers(0, 2**31 - 1))
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 256, size=(R, M, N), dtype=np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0                               # the senders clamp to +-448: no NaN codes
+    s = (rng.random((R * M, G), dtype=np.float32) * 0.05 + 1e-4).astype(np.float32)
+    return q, s, ld
+
+
+@settings(max_examples=40, deadline=None, derandomize=True)
+@given(rs_chunks())
+def test_gpu_fp8_combine_matches_oracle_on_random_chunks(case):
+    """The combine after the FP8 reduce-scatter (overlap_forward.py:932-944)."""
+    from td_benchmark_amd import ops
+    q, s, ld = case
+    R, M, N = q.shape
+    full = torch.zeros((M, ld), dtype=torch.bfloat16, device="cuda")
+    qd = torch.from_numpy(q).cuda().view(torch.float8_e4m3fn)
+    ops.fp8_dequant_sum(qd, torch.from_numpy(s).cuda(), out=full[:, :N])
+    torch.cuda.synchronize()
+    assert np.array_equal(u8_bits(full[:, :N]).view(np.uint16), oracle.fp8_dequant_sum(q, s))
