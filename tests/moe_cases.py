@@ -130,3 +130,58 @@ def e4m3_ulp_diff(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     # crossing zero: +m vs -n differ by m+n ulps
     d = np.where(opposite, ma + mb, d)
     return d
+
+
+# ---------------------------------------------------------------- A7 accounting
+
+# North-star bar on the intermediate FP8 codes against the CPU oracle chain:
+# at most 1 e4m3 ULP on at most 0.1 % of codes.
+A7_MAX_ULP = 1
+A7_MAX_FRAC = 1e-3
+
+
+def a7_account(codes: np.ndarray, scales: np.ndarray, h_gpu: np.ndarray, c13_gpu: np.ndarray | None,
+               st_q2: np.ndarray, st_s2: np.ndarray, st_h: np.ndarray, st_c13: np.ndarray | None) -> dict:
+    """Compare the path's intermediate codes/scales (row-aligned with the
+    oracle's slot-indexed ones) with the oracle chain, and trace every
+    difference to its cause.
+
+    The 1x128 quant is bit-exact given h (tested separately), so a code can
+    differ only where the GPU's h differs from the oracle's in that element or
+    in the element that sets the group's scale; h in turn differs only where
+    SiLU*up's inputs (the bf16 C13 gate and up values) differ, or, rarely,
+    where SiLU's own fp32 rounding lands on the other side of a bf16 tie.
+    Returns the rates and the counts of each cause."""
+    I = codes.shape[1]
+    d = e4m3_ulp_diff(codes, st_q2)
+    code_diff = d > 0
+    h_diff = h_gpu != st_h
+    s_diff = scales != st_s2
+    s_diff_el = np.repeat(s_diff, 128, axis=1)[:, :I]
+    untraced = code_diff & ~h_diff & ~s_diff_el
+    # a group's h differs somewhere <=> its scale may differ; a scale differing
+    # with every h of its group equal would be a quant error
+    grp_h = h_diff.reshape(h_diff.shape[0], -1, 128).any(axis=2) if I % 128 == 0 else None
+    bad_scale = int((s_diff & ~grp_h).sum()) if grp_h is not None else 0
+    rep = dict(n=int(d.size), frac=float(code_diff.mean()), max_ulp=int(d.max()) if d.size else 0,
+               n_code_diff=int(code_diff.sum()), n_h_diff=int(h_diff.sum()),
+               n_scale_diff=int(s_diff.sum()), untraced=int(untraced.sum()), bad_scale=bad_scale,
+               code_via_h=int((code_diff & h_diff).sum()),
+               code_via_scale_only=int((code_diff & ~h_diff & s_diff_el).sum()))
+    if c13_gpu is not None and st_c13 is not None:
+        gate_diff = c13_gpu[:, :I] != st_c13[:, :I]
+        up_diff = c13_gpu[:, I:] != st_c13[:, I:]
+        from_c13 = h_diff & (gate_diff | up_diff)
+        rep["h_via_c13"] = int(from_c13.sum())
+        rep["h_via_silu"] = int((h_diff & ~(gate_diff | up_diff)).sum())
+        rep["c13_diff_frac"] = float((c13_gpu != st_c13).mean())
+    return rep
+
+
+def a7_assert(rep: dict, what: str) -> None:
+    msg = (f"{what}: intermediate codes vs oracle chain: {rep['frac']:.3e} of {rep['n']} differ "
+           f"(bar {A7_MAX_FRAC:g}), max {rep['max_ulp']} ulp (bar {A7_MAX_ULP}); causes {rep}")
+    print(msg, flush=True)
+    assert rep["untraced"] == 0 and rep["bad_scale"] == 0, msg
+    assert rep["max_ulp"] <= A7_MAX_ULP, msg
+    assert rep["frac"] <= A7_MAX_FRAC, msg

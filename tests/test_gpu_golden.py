@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import oracle
-from moe_cases import bf16_bits, e4m3_ulp_diff, u8_bits
+from moe_cases import a7_account, a7_assert, bf16_bits, u8_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -108,14 +108,24 @@ def test_fused_w13_codes(fx, dev):
                                      dev["f32"](fx["w13_s"]), dev["i32"](fx["sorted_ids"]),
                                      dev["i32"](fx["expert_ids"]), dev["i32"](fx["ntpp"]), S, k, BM)
     torch.cuda.synchronize()
+    # the GPU's own C13 and h (unfused chain, same kernels) to trace differences
+    c13 = torch.zeros((S, 2 * I), dtype=torch.bfloat16, device=dev["device"])
+    ops.dispatch_fused_moe_kernel(dev["u8"](fx["q1"]), dev["u8"](fx["w13_q"]), c13, dev["f32"](fx["s1"]),
+                                  dev["f32"](fx["w13_s"]), None, None, dev["i32"](fx["sorted_ids"]),
+                                  dev["i32"](fx["expert_ids"]), dev["i32"](fx["ntpp"]), False, k,
+                                  {"BLOCK_SIZE_M": BM})
+    h = torch.empty((S, I), dtype=torch.bfloat16, device=dev["device"])
+    ops.silu_and_mul(h, c13)
+    torch.cuda.synchronize()
     codes, scales = u8_bits(hq), hs.cpu().numpy()
     pos = np.nonzero(fx["sorted_ids"][: int(fx["ntpp"][0])] < S)[0]
     slots = fx["sorted_ids"][pos]
-    ulp = e4m3_ulp_diff(codes[pos], fx["q2"][slots])
     # codes follow the GPU's own C13, which may differ from the oracle's by the
-    # MFMA accumulation bound; a flipped rounding decision moves a code by 1
-    assert ulp.max() <= 1 and np.mean(ulp > 0) <= 0.01
-    np.testing.assert_allclose(scales[pos], fx["s2"][slots], rtol=2 ** -6)
+    # MFMA accumulation bound: <= 1 ULP on <= 0.1 % of codes, each traced to a
+    # differing h or scale; scales bit-exact wherever the group's h matches
+    rep = a7_account(codes[pos], scales[pos], bf16_bits(h)[slots], bf16_bits(c13)[slots], fx["q2"][slots],
+                     fx["s2"][slots], fx["h"][slots], fx["c13"][slots])
+    a7_assert(rep, "golden tiny_seed0 fused W13")
 
 
 def test_w2_gemm_and_reduce(fx, dev):

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from moe_cases import bf16_bits, e4m3_ulp_diff, make_case, to_gpu, u8_bits
+from moe_cases import a7_account, a7_assert, bf16_bits, make_case, to_gpu, u8_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -279,11 +279,12 @@ def test_w13_fused_silu_quant(T, H, I, E, k, BM, routing):
     h_ref = oracle.silu_and_mul(bf16_bits(C))
     _bf16_close(h_np, h_ref, ulps=1)
     assert (h_np != h_ref).mean() <= 1e-3
-    # 4) against the all-CPU chain (exact dots): report, and bound the tail
-    d = e4m3_ulp_diff(hq_np, st["q2"][slots])
-    frac = (d > 0).mean()
-    _log(f"codes vs CPU chain: differ {frac:.2e}, >1ulp {(d > 1).mean():.2e}, max {d.max()}")
-    assert frac <= 1e-2
+    # 4) against the all-CPU chain (exact dots): the north-star bar (<= 1 e4m3
+    #    ULP on <= 0.1 % of codes), every differing code traced to a differing
+    #    h or group scale, and each differing h to its C13 inputs or to SiLU
+    rep = a7_account(hq_np, hs_np, h_np[slots], bf16_bits(C)[slots], st["q2"][slots], st["s2"][slots],
+                     st["h"][slots], st["c13"][slots])
+    a7_assert(rep, f"w13 fused T={T} H={H} I={I} E={E} k={k} BM={BM}")
 
 
 @pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
@@ -360,3 +361,48 @@ def test_reduce_topk_bit_exact(T, k, H):
     ops.moe_sum(dD, y, k)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bf16_bits(y), ref)
+
+
+@pytest.mark.parametrize("tile_m", [0, 16, 64])
+def test_grouped_gemm_runs_longer_than_65_blocks(tile_m):
+    """Runs of more than 65 align blocks of one expert (two experts share 4096
+    slots at block size 16, about 128 blocks each): the kernel's run search
+    continues past the 64 blocks it loads in its first round trip
+    (overlap/kernels.py:95-126, block -> expert).  W13 plain and W2 routed
+    against the oracle, at the automatic tile height (256 rows), one block per
+    tile, and four blocks per tile."""
+    from tile_map import runs_of
+    ops = _ops()
+    T, H, I, E, k, BM = 4096, 256, 256, 2, 1, 16
+    c = make_case(T, H, I, E, k, BM, seed=77)
+    q1, s1 = oracle.quant_group128(c.x)
+    sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, E, BM)
+    runs = [n for _, n in runs_of(eids[: ntpp // BM])]
+    assert max(runs) > 65, runs
+    _log(f"long runs {runs} tile_m={tile_m}")
+    ref, mag = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
+                                   with_magnitude=True)
+    g = to_gpu(c)
+    dq = torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn)
+    ds = torch.from_numpy(s1).cuda()
+    d_sorted = torch.from_numpy(sorted_ids).cuda()
+    d_eids = torch.from_numpy(eids).cuda()
+    d_ntpp = torch.tensor([ntpp], dtype=torch.int32, device="cuda")
+    C = torch.zeros((c.S, 2 * I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(dq, g["w13"], C, ds, g["w13_s"], None, None, d_sorted, d_eids, d_ntpp,
+                                  False, k, {"BLOCK_SIZE_M": BM}, tile_m=tile_m)
+    # W2 on seeded codes by sorted position, routed weights applied
+    rng = np.random.default_rng(6)
+    mp = sorted_ids.size
+    hq = rng.integers(0, 256, size=(mp, I), dtype=np.uint8)
+    hq[(hq & 0x7F) == 0x7F] = 0
+    hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
+    ref2, mag2 = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
+                                     a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_magnitude=True)
+    D = torch.zeros((c.S, H), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(torch.from_numpy(hq).cuda().view(torch.float8_e4m3fn), g["w2"], D,
+                                  torch.from_numpy(hs).cuda(), g["w2_s"], None, g["topk_w"].view(-1), d_sorted,
+                                  d_eids, d_ntpp, True, 1, {"BLOCK_SIZE_M": BM}, a_by_pos=True, tile_m=tile_m)
+    torch.cuda.synchronize()
+    _gemm_close(bf16_bits(C), ref, mag)
+    _gemm_close(bf16_bits(D), ref2, mag2)
