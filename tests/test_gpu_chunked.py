@@ -152,15 +152,23 @@ def test_k_split_first_chunk_with_presliced_a_equals_window_gemm():
     assert np.array_equal(bf16_bits(C), bf16_bits(ref))
 
 
-@pytest.mark.parametrize("T", [200, 700])   # one-launch and three-launch align paths
-def test_expert_map_equals_local_problem(T):
+# (T, E, k, local experts): one-launch and three-launch align paths; and 64
+# global experts with the local ones first or last, so the blocks of the 60
+# non-local experts form one run of about 150 expert -1 blocks, longer than the
+# 65 blocks the GEMM's run search covers in its first round trip
+EP_CASES = {"t200": (200, 8, 2, [2, 5, 6]), "t700": (700, 8, 2, [2, 5, 6]),
+            "long_run_after": (512, 64, 4, [0, 1, 2, 3]), "long_run_before": (512, 64, 4, [60, 61, 62, 63])}
+
+
+@pytest.mark.parametrize("case", sorted(EP_CASES))
+def test_expert_map_equals_local_problem(case):
     import torch
 
     from td_benchmark_amd import ops
 
-    print(f"case: expert_map T={T}", flush=True)
-    c = make_case(T=T, H=256, I=256, E=8, k=2, BM=16, seed=33)
-    local = [2, 5, 6]
+    T, E, k, local = EP_CASES[case]
+    print(f"case: expert_map {case} T={T} E={E} k={k} local={local}", flush=True)
+    c = make_case(T=T, H=256, I=256, E=E, k=k, BM=16, seed=33)
     emap = np.full(c.E, -1, np.int32)
     emap[local] = np.arange(len(local), dtype=np.int32)
     g = to_gpu(c)
@@ -187,3 +195,8 @@ def test_expert_map_equals_local_problem(T):
     assert int(ntpp.item()) == ntpp_ref
     mapped = np.where(eids_ref[:nb] >= 0, emap[np.maximum(eids_ref[:nb], 0)], -1)
     assert np.array_equal(eids.cpu().numpy()[:nb], mapped)
+    if case.startswith("long_run"):
+        from tile_map import runs_of
+        minus = [n for b, n in runs_of(mapped) if mapped[b] < 0]
+        print(f"  expert -1 runs {minus}", flush=True)
+        assert max(minus) > 65

@@ -141,17 +141,27 @@ def test_layer_with_shared_expert_meets_golden_gates():
     assert np.array_equal(bf16_bits(y), bf16_bits(y_ref))
 
 
+# (T, E, k, BM): 32-row tiles per chunk; and chunks whose experts average
+# >= 160 slots (S_chunk >= 160 E), so every chunk runs 256-row tiles over
+# 64-row blocks with the activation scales by sorted position
+CHUNK_SETUPS = {"short": (301, 8, 4, 32), "tall": (1600, 4, 2, 64)}
+
+
+@pytest.mark.parametrize("setup", sorted(CHUNK_SETUPS))
 @pytest.mark.parametrize("n_chunks,n_streams", [(4, 2), (3, 1), (2, 2)])
-def test_chunked_runner_equals_single_pass(n_chunks, n_streams):
+def test_chunked_runner_equals_single_pass(n_chunks, n_streams, setup):
     torch = _torch()
     from td_benchmark_amd import ops
 
-    print(f"case: chunked runner {n_chunks}x{n_streams}", flush=True)
-    c = make_case(T=301, H=256, I=256, E=8, k=4, BM=32, seed=11)
+    T, E, k, BM = CHUNK_SETUPS[setup]
+    print(f"case: chunked runner {n_chunks}x{n_streams} {setup} T={T} E={E} k={k} BM={BM}", flush=True)
+    c = make_case(T=T, H=256, I=256, E=E, k=k, BM=BM, seed=11)
     g = to_gpu(c)
-    one = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 32)
+    one = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, BM)
     y1 = bf16_bits(one.run(g["x"], g["topk_w"].view(-1), g["topk_ids"].view(-1)))
-    ch = ops.ChunkedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, n_chunks, n_streams, 32)
+    ch = ops.ChunkedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, n_chunks, n_streams, BM)
+    if setup == "tall" and n_chunks <= 4:
+        assert all(ops.gemm_tile_rows(r.BM, r.S, r.E) == 256 and r.scales_by_position for r in ch.runners)
     for _ in range(2):
         y2 = ch.run(g["x"], g["topk_w"], g["topk_ids"])
         torch.cuda.synchronize()
@@ -200,6 +210,53 @@ def test_scheme_m1_run_meets_golden_gates(tunables):
     inst.close()
     with pytest.raises(RuntimeError, match="closed"):
         inst.run()
+
+
+@pytest.mark.parametrize("tunables", [{}, {"n_chunks": 3, "n_streams": 2}])
+def test_scheme_run_allocates_nothing(tunables):
+    """The builder allocates every buffer; run() only launches kernels
+    (schemes/base.py:45-93; the reference's own lesson on allocation inside the
+    timed call, docs/exp/EXP-024-cgroup-perf-rootcause.md:6-9).  With a shared
+    expert whose runner was built for a larger row count than a chunk holds,
+    run() still allocates nothing: the align outputs for the chunk's rows are
+    prepared at build time."""
+    torch = _torch()
+    from td_benchmark_amd import schemes
+
+    print(f"case: scheme m1 allocation-free run {tunables}", flush=True)
+    c, s1, s2 = _shared_case(12)
+    g = to_gpu(c)
+    ctx = SimpleNamespace(rank=0, world_size=1, device=torch.device("cuda", 0))
+    inst = schemes.build_scheme(None, ctx, _bundle(c, g, (s1, s2)), SimpleNamespace(code="m1", tunables=tunables))
+    inst.run()  # lazy instances build on the first call
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_stats()["allocation.all.allocated"]
+    for _ in range(3):
+        inst.run()
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_stats()["allocation.all.allocated"]
+    assert after == before, f"run() allocated {after - before} blocks"
+    inst.close()
+
+
+def test_shared_expert_rejects_unprepared_row_counts():
+    torch = _torch()
+    from td_benchmark_amd import ops
+
+    print("case: shared expert row counts", flush=True)
+    c, s1, s2 = _shared_case(12)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    sh = ops.SharedExpertRunner(dev(s1[0]).view(ops.FP8), dev(s1[1]), dev(s2[0]).view(ops.FP8), dev(s2[1]), c.T,
+                                row_counts=(c.T // 2,))
+    x = to_gpu(c)["x"]
+    y_half = sh(x[: c.T // 2].contiguous()).clone()
+    y_full = sh(x)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(y_half), bf16_bits(y_full[: c.T // 2]))
+    with pytest.raises(ValueError, match="no align outputs prepared"):
+        sh(x[: c.T // 3].contiguous())
+    with pytest.raises(ValueError, match="exceed max_tokens"):
+        sh.prepare(c.T + 1)
 
 
 @pytest.mark.parametrize("name", ["mb_moe_align", "mb_quant_kernels", "mb_group_gemm",

@@ -108,3 +108,26 @@ def test_sampled_tokens_meet_the_golden_gates(layer):
     rep = oracle.compare_outputs(got, ref, atol=0.0, rtol=0.0)
     print(f"  fp32 on the consumed operands: max-abs-rel {rep['max_abs_rel']:.4f}", flush=True)
     assert rep["max_abs_rel"] <= oracle.MAX_ABS_REL, rep
+
+
+def test_chunked_pipeline_equals_one_pass(layer):
+    """Config 5 at its own size: the 4-chunk x 2-stream pipeline of the Qwen3
+    layer (T=16384; every chunk's experts average 256 slots, so each chunk runs
+    256-row tiles with the activation scales by sorted position) gives the
+    one-pass runner's output bit for bit, on two runs in a row
+    (overlap_forward.py:252-342: chunks on side streams, joined before return)."""
+    wl, d, runner, y = layer
+    if wl.n_chunks <= 1:
+        pytest.skip("only the chunked configuration")
+    from td_benchmark_amd import ops
+    ch = ops.ChunkedExpertsRunner(d.w13, d.w13_s, d.w2, d.w2_s, wl.T, wl.top_k, wl.n_chunks, wl.n_streams,
+                                  wl.block_m)
+    tm = [ops.gemm_tile_rows(r.BM, r.S, r.E, r.tile_m) for r in ch.runners]
+    print(f"  chunks {ch.bounds}, tile heights {tm}, scales by position "
+          f"{[r.scales_by_position for r in ch.runners]}", flush=True)
+    assert all(t == 256 for t in tm) and all(r.scales_by_position for r in ch.runners)
+    want = bf16_bits(y)
+    for _ in range(2):
+        got = ch.run(d.x, d.topk_w, d.topk_ids)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(got), want)

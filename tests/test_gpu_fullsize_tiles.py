@@ -1,0 +1,132 @@
+"""GPU: whole output tiles of the full-size DeepSeek-V3 and Mixtral layers
+against the CPU oracle.
+
+The layers are too large for the oracle to run whole, so the check picks
+complete workgroup tiles of each grouped GEMM launch (tests/tile_map.py):
+the first and last active tile of every XCD's range of the expert-major
+order, and both parts of a run split unevenly over its row tiles (a one-block
+tile and the larger last tile holding the run's padding).  For each picked
+tile every valid row and every column of its n-tile is compared:
+* W13 as a plain GEMM (C13 bf16 by slot) with the accumulation bound of the
+  GEMM tests, |d| <= 2^-7 |ref| + 2^-12 L1 (overlap/kernels.py:95-214);
+* the fused W13 epilogue's FP8 codes and scales of the same rows and group
+  against the oracle chain (silu_and_mul + 1x128 quant of the oracle's C13,
+  overlap_forward.py:277-284) at <= 1 e4m3 ULP on <= 0.1 % of codes, each
+  differing code traced to a differing h or scale of the GPU's own chain;
+* W2 with routed weights (D bf16 by slot, A rows and scales by sorted
+  position) on its own tile map, same bound (overlap_forward.py:289-302).
+The oracle runs on the tile's expert and columns only: the other positions of
+the sorted order are set to the pad value S, so the oracle skips them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from moe_cases import a7_account, a7_assert, bf16_bits, u8_bits
+from tile_map import pick_tiles, tile_map, tile_positions
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", params=["dsv3", "mixtral"])
+def layer(request):
+    from td_benchmark_amd import ops, workloads
+    wl = workloads.CONFIGS[request.param]
+    print(f"case: full-size tiles {wl.name}", flush=True)
+    d = workloads.generate(wl, "cuda")
+    runner = ops.FusedExpertsRunner(d.w13, d.w13_s, d.w2, d.w2_s, wl.T, wl.top_k, wl.block_m)
+    runner.run(d.x, d.topk_w, d.topk_ids)
+    a = runner.align
+    # W13 as a plain GEMM, and the GPU's own unfused chain, for tracing
+    C13 = torch.empty((wl.S, 2 * wl.I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(runner.q1, d.w13, C13, runner.s1, d.w13_s, None, None, a.sorted_ids, a.expert_ids,
+                                  a.ntpp, False, wl.top_k, {"BLOCK_SIZE_M": wl.block_m})
+    h = torch.empty((wl.S, wl.I), dtype=torch.bfloat16, device="cuda")
+    ops.silu_and_mul(h, C13)
+    torch.cuda.synchronize()
+    ntpp = int(a.ntpp.item())
+    host = dict(
+        sorted=a.sorted_ids.cpu().numpy(), eids=a.expert_ids.cpu().numpy(), ntpp=ntpp,
+        q1=u8_bits(runner.q1), s1=runner.s1.cpu().numpy(),
+        hq=u8_bits(runner.hq), hs=np.ascontiguousarray(runner.hs.cpu().numpy()),
+        topk_w=d.topk_w.cpu().numpy().ravel())
+    tile_m = ops.gemm_tile_rows(runner.BM, runner.S, runner.E, runner.tile_m)
+    print(f"  ntpp {ntpp}, tile height {tile_m}", flush=True)
+    return wl, d, runner, C13, h, host, tile_m
+
+
+def _expert_cols(w: torch.Tensor, ws: torch.Tensor, e: int, groups: list[int]):
+    """Expert e's weight rows of the given 128-row scale groups, as a
+    one-expert operand for the oracle: (fp8 [1, 128*len(groups), K], scales)."""
+    q = torch.cat([w[e, g * 128:(g + 1) * 128] for g in groups]).view(torch.uint8).cpu().numpy()[None]
+    s = ws[e, groups].cpu().numpy()[None]
+    return np.ascontiguousarray(q), np.ascontiguousarray(s)
+
+
+def _only(host, ti, BM):
+    """The sorted order with every position outside the tile set to the pad
+    value, and the block ids with the tile's blocks on (local) expert 0."""
+    S = host["topk_w"].size
+    srt = np.full_like(host["sorted"], S)
+    p = np.arange(ti.pos0, ti.pos0 + ti.rows)
+    srt[p] = host["sorted"][p]
+    eids = np.full_like(host["eids"], -1)
+    eids[ti.pos0 // BM:(ti.pos0 + ti.rows) // BM] = 0
+    return srt, eids
+
+
+def test_w13_whole_tiles(layer):
+    wl, d, runner, C13, h, host, tile_m = layer
+    S, I, BM = wl.S, wl.I, wl.block_m
+    tiles = tile_map(host["eids"], host["ntpp"], BM, tile_m, I // 128)
+    picked = pick_tiles(tiles, host["sorted"], S)
+    c13 = bf16_bits(C13)
+    h_gpu = bf16_bits(h)
+    for name, ti in picked.items():
+        pos = tile_positions(ti, host["sorted"], S)
+        slots = host["sorted"][pos]
+        srt, eids = _only(host, ti, BM)
+        # plain W13: scale groups 2j and 2j+1
+        groups = [2 * ti.j, 2 * ti.j + 1]
+        B, Bs = _expert_cols(d.w13, d.w13_s, ti.expert, groups)
+        ref, mag = oracle.grouped_gemm(host["q1"], host["s1"], B, Bs, srt, eids, host["ntpp"], BM, S, wl.top_k,
+                                       with_magnitude=True)
+        got = c13[slots][:, 256 * ti.j:256 * ti.j + 256]
+        bad = oracle.gemm_close(got, ref[slots], mag[slots])
+        print(f"  W13 {name}: {ti} rows {pos.size}, outside bound {int(bad.sum())}", flush=True)
+        assert not bad.any(), f"W13 tile {name}: {int(bad.sum())} of {bad.size} outside the bound"
+        # fused codes of group j: gate group j and up group I/128 + j
+        fgroups = [ti.j, I // 128 + ti.j]
+        B, Bs = _expert_cols(d.w13, d.w13_s, ti.expert, fgroups)
+        cref = oracle.grouped_gemm(host["q1"], host["s1"], B, Bs, srt, eids, host["ntpp"], BM, S, wl.top_k)[slots]
+        href = oracle.silu_and_mul(cref)
+        qref, sref = oracle.quant_group128(href)
+        cols = np.r_[128 * ti.j:128 * ti.j + 128]
+        c_gpu = np.concatenate([c13[slots][:, cols], c13[slots][:, I + cols]], axis=1)
+        rep = a7_account(host["hq"][pos][:, cols], host["hs"][pos][:, ti.j:ti.j + 1], h_gpu[slots][:, cols], c_gpu,
+                         qref, sref, href, cref)
+        a7_assert(rep, f"{wl.name} fused W13 tile {name}")
+
+
+def test_w2_whole_tiles(layer):
+    wl, d, runner, C13, h, host, tile_m = layer
+    S, H, BM = wl.S, wl.H, wl.block_m
+    n_tiles = (H // 128 + 1) // 2
+    tiles = tile_map(host["eids"], host["ntpp"], BM, tile_m, n_tiles)
+    picked = pick_tiles(tiles, host["sorted"], S)
+    D = bf16_bits(runner.D[:S])
+    for name, ti in picked.items():
+        pos = tile_positions(ti, host["sorted"], S)
+        slots = host["sorted"][pos]
+        srt, eids = _only(host, ti, BM)
+        groups = [g for g in (2 * ti.j, 2 * ti.j + 1) if g < H // 128]
+        B, Bs = _expert_cols(d.w2, d.w2_s, ti.expert, groups)
+        ref, mag = oracle.grouped_gemm(host["hq"], host["hs"], B, Bs, srt, eids, host["ntpp"], BM, S, 1,
+                                       a_row_by_pos=True, topk_w=host["topk_w"], with_magnitude=True)
+        got = D[slots][:, 256 * ti.j:256 * ti.j + 128 * len(groups)]
+        bad = oracle.gemm_close(got, ref[slots], mag[slots])
+        print(f"  W2 {name}: {ti} rows {pos.size}, outside bound {int(bad.sum())}", flush=True)
+        assert not bad.any(), f"W2 tile {name}: {int(bad.sum())} of {bad.size} outside the bound"

@@ -7,7 +7,10 @@ import subprocess
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
+
+import oracle
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -88,3 +91,71 @@ def test_gemm_tile_rows_rule():
     assert ops.gemm_tile_rows(64, 160 * 8, 8) == 256       # the threshold itself
     assert ops.gemm_tile_rows(64, 160 * 8 - 1, 8) == 64
     assert ops.gemm_tile_rows(64, 16, 8, tile_m=128) == 128
+
+
+@pytest.mark.parametrize("T,E,k,BM,tile_m,n_tiles,routing", [
+    (8192, 256, 8, 128, 256, 16, "sigmoid"),   # DSv3 W13
+    (8192, 256, 8, 128, 256, 28, "sigmoid"),   # DSv3 W2
+    (4096, 8, 2, 128, 256, 112, "softmax"),    # Mixtral W13
+    (128, 256, 8, 32, 32, 16, "zipf"),         # decode
+    (4096, 2, 1, 16, 256, 1, "softmax"),       # runs longer than 65 blocks
+])
+def test_tile_map_covers_every_position_once(T, E, k, BM, tile_m, n_tiles, routing):
+    """The host restatement of the GEMM's tile mapping (tests/tile_map.py)
+    partitions the sorted positions x n-tiles: every (position, n-tile) of the
+    padded order lies in exactly one active tile, tiles stay inside one run,
+    and each XCD range is contiguous."""
+    from moe_cases import route
+    from tile_map import XCDS, pick_tiles, tile_map
+    rng = np.random.default_rng(T + E)
+    ids, _ = route(rng.standard_normal((T, E), dtype=np.float32), k, routing, rng)
+    srt, eids, ntpp = oracle.moe_align(ids, E, BM)
+    tiles = tile_map(eids, ntpp, BM, tile_m, n_tiles)
+    cov = np.zeros((ntpp, n_tiles), np.int32)
+    for ti in tiles:
+        assert ti.rows % BM == 0 and 0 < ti.rows <= max(tile_m, BM)
+        assert len(set(eids[ti.pos0 // BM:(ti.pos0 + ti.rows) // BM].tolist())) == 1
+        cov[ti.pos0:ti.pos0 + ti.rows, ti.j] += 1
+    assert cov.min() == 1 and cov.max() == 1
+    ts = sorted(t.t for t in tiles)
+    assert len(set(ts)) == len(ts) and max(t.xcd for t in tiles) < XCDS
+    picked = pick_tiles(tiles, srt, T * k)
+    assert {f"xcd{x}_first" for x in {t.xcd for t in tiles}} <= set(picked)
+
+
+def test_bench_summarize_samples_follows_reference_statistics():
+    """avg/min/med/p95/std as moe_bench/timing.py:23-34 defines them (p95 at
+    index int(0.95 * (n - 1)) of the sorted samples, population std)."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    s = bench.summarize_samples([5.0, 1.0, 3.0, 2.0, 4.0])
+    assert s["avg"] == 3.0 and s["min"] == 1.0 and s["med"] == 3.0
+    assert s["p95"] == 4.0  # sorted[int(0.95 * 4)] = sorted[3]
+    assert abs(s["std"] - 2.0 ** 0.5) < 1e-12
+    assert bench.summarize_samples([])["n"] == 0
+
+
+def test_bench_cpu_baseline_runs_the_torch_golden_on_all_cores():
+    """The CPU baseline leg on the tiny configuration, with CPU tensors in
+    place of the GPU workload: torch threads = os.cpu_count(), the lscpu model
+    name, and the stage timings of the torch ops."""
+    import os
+
+    import torch
+
+    from moe_cases import make_case
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from td_benchmark_amd import workloads
+    wl = workloads.CONFIGS["tiny"]
+    c = make_case(wl.T, wl.H, wl.I, wl.E, wl.top_k, wl.block_m, seed=0)
+    f8 = lambda a: torch.from_numpy(a).view(torch.float8_e4m3fn)  # noqa: E731
+    data = workloads.LayerData(torch.from_numpy(c.x.view(np.int16)).view(torch.bfloat16),
+                               torch.from_numpy(c.topk_ids), torch.from_numpy(c.topk_w),
+                               f8(c.w13_q), torch.from_numpy(c.w13_s), f8(c.w2_q), torch.from_numpy(c.w2_s))
+    cb = bench.cpu_baseline(data, wl, budget_s=0.2)
+    assert cb["value"] > 0 and cb["cores"] == os.cpu_count() and cb["kind"] == "port"
+    assert cb["cpu_model"]
+    D = torch.zeros((wl.S, wl.H), dtype=torch.bfloat16)
+    st = bench.cpu_stage_times(data, wl, D, wl.block_m)
+    assert st["quant_us"] > 0 and st["align_us"] > 0 and st["reduce_us"] > 0
