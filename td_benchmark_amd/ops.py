@@ -554,10 +554,17 @@ class SharedExpertRunner:
     1x128 first; an FP8 ``x`` is used directly with its [rows, H/128]
     ``input_scale`` -- no dequantise/requantise round trip
     (shared_expert.py:3-7, 83-93).  Returns a [rows, H] bf16 view of an
-    internal buffer (valid until the next call)."""
+    internal buffer (valid until the next call).
+
+    Every buffer is allocated when the runner is built (the builder-allocates
+    contract of schemes/base.py:45-93): the align outputs exist for
+    ``max_tokens`` rows and for each count in ``row_counts``, or added later
+    with ``prepare(rows)``; a call with any other row count raises instead of
+    allocating."""
 
     def __init__(self, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
-                 w2_scale: torch.Tensor, max_tokens: int, block_size_m: int | None = None):
+                 w2_scale: torch.Tensor, max_tokens: int, block_size_m: int | None = None,
+                 row_counts: tuple[int, ...] = ()):
         E1, N2, H = _need_weights(w1, w1_scale, "w1")
         _need_weights(w2, w2_scale, "w2")
         if E1 != 1 or w2.shape[0] != 1:
@@ -569,7 +576,8 @@ class SharedExpertRunner:
         self.BM = block_size_m or get_moe_config(max_tokens, 1, 1)["BLOCK_SIZE_M"]
         dev = w1.device
         self._aligns: dict[int, AlignBuffers] = {}
-        self._align_for(max_tokens)
+        for rows in (max_tokens, *row_counts):
+            self.prepare(rows)
         mp = self._aligns[max_tokens].max_padded
         self.q = torch.empty((max_tokens, H), dtype=FP8, device=dev)
         self.s = torch.empty((max_tokens, H // 128), dtype=torch.float32, device=dev)
@@ -577,13 +585,21 @@ class SharedExpertRunner:
         self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
         self.out = torch.empty((max_tokens, H), dtype=torch.bfloat16, device=dev)
 
-    def _align_for(self, rows: int) -> AlignBuffers:
-        """Align outputs for `rows` tokens routed to expert 0 (built once per row count)."""
-        a = self._aligns.get(rows)
-        if a is None:
+    def prepare(self, rows: int) -> None:
+        """Build the align outputs for calls with ``rows`` tokens, all routed
+        to expert 0 (build time: this allocates and launches the align)."""
+        if rows > self.max_tokens:
+            raise ValueError(f"{rows} rows exceed max_tokens={self.max_tokens}")
+        if rows not in self._aligns:
             a = AlignBuffers(rows, 1, self.BM, self.w1.device)
             a.run(torch.zeros(rows, dtype=torch.int32, device=self.w1.device))
             self._aligns[rows] = a
+
+    def _align_for(self, rows: int) -> AlignBuffers:
+        a = self._aligns.get(rows)
+        if a is None:
+            raise ValueError(f"no align outputs prepared for {rows} rows (prepared: {sorted(self._aligns)}); "
+                             "call prepare(rows) when building the runner")
         return a
 
     def __call__(self, x: torch.Tensor, input_scale: torch.Tensor | None = None) -> torch.Tensor:
@@ -655,6 +671,8 @@ class FusedExpertsRunner:
             raise ValueError(f"tile_m must be a multiple of block_size_m in {SUPPORTED_BLOCK_M}")
         if shared is not None and (shared.H != H or shared.max_tokens < num_tokens):
             raise ValueError("shared expert does not match the layer's hidden size / token count")
+        if shared is not None:
+            shared.prepare(num_tokens)
         self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
         self.shared = shared
         self.shared_out: torch.Tensor | None = None
