@@ -11,8 +11,10 @@ Prints ONE JSON line.  ``value`` = algorithmic grouped-GEMM FLOP (6*S*H*I) per
 second over the whole timed layer (quant/align/reduce included); per-stage
 times come from HIP events recorded on the launch stream inside the timed
 region.  ``roofline`` describes the dominant kernel (the W13 GEMM).
-``cpu_baseline`` times the CPU restatement of the reference's torch golden
-(oracle.golden_moe) on a bounded sample of the same workload.
+``layer_us_stats`` gives avg/min/med/p95/std over the per-step samples
+(moe_bench/timing.py:23-34).  ``cpu_baseline`` times the reference's torch CPU
+golden path (restated in oracle/golden_torch.py, all host cores) on a bounded
+sample of the same workload.
 """
 from __future__ import annotations
 
@@ -63,89 +65,123 @@ def measured_traffic(workload: str, kernel: str) -> tuple[float | None, str | No
     return None, None
 
 
+def summarize_samples(samples_ms: list[float]) -> dict[str, float]:
+    """avg/min/med/p95/std of per-step samples, the statistics of the
+    reference's timing harness (moe_bench/timing.py:23-34)."""
+    import statistics
+    if not samples_ms:
+        return {"avg": 0.0, "min": 0.0, "med": 0.0, "p95": 0.0, "std": 0.0, "n": 0}
+    ordered = sorted(samples_ms)
+    return {"avg": statistics.mean(samples_ms), "min": ordered[0], "med": statistics.median(samples_ms),
+            "p95": ordered[min(len(ordered) - 1, int(0.95 * (len(ordered) - 1)))],
+            "std": statistics.pstdev(samples_ms) if len(samples_ms) > 1 else 0.0, "n": len(samples_ms)}
+
+
+def cpu_model_name() -> str:
+    """The host CPU's model name as lscpu reports it (/proc/cpuinfo if lscpu
+    is unavailable)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _time_cpu(fn, warmup: int, repeat: int) -> dict:
+    """bench_cpu semantics (moe_bench/timing.py:37-45): warmup calls, then
+    ``repeat`` timed calls with time.perf_counter."""
+    for _ in range(warmup):
+        fn()
+    samples = []
+    for _ in range(repeat):
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    return summarize_samples(samples)
+
+
 def cpu_stage_times(data, wl, D_sample, block_m: int) -> dict:
-    """The layer's quant, align and reduce stages on the host, single-threaded
-    C restatements from the oracle: quant over all T tokens, align over all S
-    slots, reduce over the first D_sample.shape[0] // k tokens' rows of the
-    GPU's D (extrapolated to T)."""
-    import numpy as np
+    """The layer's quant, align and reduce stages as the reference's torch CPU
+    ops (oracle/golden_torch.py), warmup 1 and repeat 3: quant over all T
+    tokens, align over all S slots, reduce over the first D_sample rows'
+    tokens (extrapolated to T)."""
+    import torch
 
-    import oracle
+    from oracle.golden_torch import align_torch, quant_group128_torch, reduce_torch
 
-    oracle.lib()  # load the library outside the timed calls
-    out = {}
-    x = data.x.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
-    ids = data.topk_ids.cpu().numpy()
-    t0 = time.perf_counter()
-    oracle.quant_group128(x)
-    out["quant_us"] = (time.perf_counter() - t0) * 1e6
-    t0 = time.perf_counter()
-    oracle.moe_align(ids, wl.E, block_m)
-    out["align_us"] = (time.perf_counter() - t0) * 1e6
+    x = data.x.cpu()
+    ids = data.topk_ids.cpu()
     tr = D_sample.shape[0] // wl.top_k
-    t0 = time.perf_counter()
-    oracle.moe_reduce(D_sample[: tr * wl.top_k], tr, wl.top_k)
-    out["reduce_us"] = (time.perf_counter() - t0) * 1e6 * wl.T / max(tr, 1)
-    out["sample"] = (f"quant {wl.T}x{wl.H}, align {wl.S} slots, reduce {tr} of {wl.T} tokens "
-                     "(scaled to T); one thread each")
-    return out
+    D = D_sample[: tr * wl.top_k]
+    q = _time_cpu(lambda: quant_group128_torch(x), 1, 3)
+    a = _time_cpu(lambda: align_torch(ids, wl.E, block_m), 1, 3)
+    r = _time_cpu(lambda: reduce_torch(D, tr, wl.top_k), 1, 3)
+    return {"quant_us": q["med"] * 1e3, "align_us": a["med"] * 1e3,
+            "reduce_us": r["med"] * 1e3 * wl.T / max(tr, 1),
+            "threads": torch.get_num_threads(),
+            "sample": (f"torch CPU ops, median of 3 after 1 warmup: quant {wl.T}x{wl.H}, align {wl.S} slots, "
+                       f"reduce {tr} of {wl.T} tokens (scaled to T)")}
 
 
 def cpu_baseline(data, wl, budget_s: float) -> dict:
-    """Time oracle.golden_moe (the reference's fp32 per-expert torch CPU path,
-    restated in numpy) on whole experts of this workload until ``budget_s`` of
-    compute has run; report its GEMM TFLOP/s and the extrapolated layer time."""
-    import numpy as np
+    """The reference's torch CPU golden path (moe_bench/verify.py:14-47,
+    restated in oracle/golden_torch.py) with torch.set_num_threads(os.cpu_count()):
+    weights dequantised one expert at a time outside the timed calls, one
+    expert's fp32 chain warmed up, then whole experts timed until ``budget_s``
+    of compute has run.  Reports its GEMM TFLOP/s and the layer time
+    extrapolated to every slot."""
+    import torch
 
-    import oracle
+    from oracle.golden_torch import dequant_expert_torch, golden_moe_torch
 
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([int(i.get("num_threads", 1)) for i in threadpool_info()
-                       if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = 1
-    ids = data.topk_ids.cpu().numpy()
-    wts = data.topk_w.cpu().numpy()
-    x = data.x.float().cpu().numpy()
-    counts = np.bincount(ids.ravel(), minlength=wl.E)
-    order = np.random.default_rng(0).permutation(wl.E)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    ids = data.topk_ids.cpu()
+    wts = data.topk_w.cpu()
+    x = data.x.float().cpu()
+    counts = torch.bincount(ids.view(-1).long(), minlength=wl.E)
+    order = [int(e) for e in torch.randperm(wl.E, generator=torch.Generator().manual_seed(0)) if counts[e] > 0]
+
+    def weights(e):
+        w1 = dequant_expert_torch(data.w13[e].cpu(), data.w13_s[e].cpu())
+        w2 = dequant_expert_torch(data.w2[e].cpu(), data.w2_s[e].cpu())
+        return w1, w2
+
+    out = torch.zeros((wl.T, wl.H), dtype=torch.float32)
+    w1, w2 = weights(order[0])
+    golden_moe_torch(x, ids, wts, lambda _e: w1, lambda _e: w2, experts=[order[0]], out=out)  # warmup
     t_total, slots, done = 0.0, 0, 0
     for e in order:
-        if counts[e] == 0:
-            continue
-        w1 = oracle.bf16_to_f32(oracle.dequant_block128(
-            data.w13[e:e + 1].contiguous().view(__import__("torch").uint8).cpu().numpy(),
-            data.w13_s[e:e + 1].cpu().numpy()))[0]
-        w2 = oracle.bf16_to_f32(oracle.dequant_block128(
-            data.w2[e:e + 1].contiguous().view(__import__("torch").uint8).cpu().numpy(),
-            data.w2_s[e:e + 1].cpu().numpy()))[0]
+        w1, w2 = weights(e)
         t0 = time.perf_counter()
-        oracle.golden_moe(x, ids, wts, lambda _e: w1, lambda _e: w2, experts=[e])
+        golden_moe_torch(x, ids, wts, lambda _e: w1, lambda _e: w2, experts=[e], out=out)
         t_total += time.perf_counter() - t0
         slots += int(counts[e])
         done += 1
         if t_total >= budget_s:
             break
     flop = 6.0 * slots * wl.H * wl.I
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {
         "value": flop / t_total / 1e12,
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle.golden_moe (fp32 numpy/BLAS restatement of verify.py:14-47) on {done} of "
-                   f"{int((counts > 0).sum())} active experts ({slots} of {wl.S} slots), {t_total:.1f} s"),
+        "sample": (f"torch CPU restatement of verify.py:14-47 (oracle/golden_torch.py), "
+                   f"torch.set_num_threads({cores}), on {done} of {len(order)} active experts "
+                   f"({slots} of {wl.S} slots), {t_total:.1f} s after one warmup expert"),
         "layer_us_extrapolated": t_total / max(slots, 1) * wl.S * 1e6,
-        "cpu_model": model,
-        "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model_name(),
+        "host_cpus": cores,
     }
 
 
@@ -214,6 +250,12 @@ def main() -> int:
     ms_single = ms_per_step
     stage_ms = {name: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
                 for j, name in enumerate(STAGES)}
+    # per-step samples: each step's first to last event (the gaps between
+    # steps, a few microseconds of launch, fall outside them)
+    single_stats = summarize_samples([ev[0].elapsed_time(ev[-1]) * 1e3 for ev in events])
+    stage_stats = {name: summarize_samples([ev[j].elapsed_time(ev[j + 1]) * 1e3 for ev in events])
+                   for j, name in enumerate(STAGES) if name in ("w13", "w2")}
+    step_stats = single_stats
     # The same layer replayed from a captured HIP graph (one launch per step);
     # shows the launch overhead that matters for the small configurations.
     ms_graph = None
@@ -232,12 +274,17 @@ def main() -> int:
         for _ in range(args.warmup):
             pipe.run(data.x, data.topk_w, data.topk_ids)
         torch.cuda.synchronize()
+        pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
         start.record()
-        for _ in range(args.steps):
+        for i in range(args.steps):
+            pev[i][0].record()
             pipe.run(data.x, data.topk_w, data.topk_ids)
+            pev[i][1].record()
         end.record()
         torch.cuda.synchronize()
         ms_per_step = start.elapsed_time(end) / args.steps
+        step_stats = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in pev])
 
     ntpp = int(runner.align.ntpp.item())
     counts = torch.bincount(data.topk_ids.view(-1).long(), minlength=wl.E)
@@ -291,7 +338,10 @@ def main() -> int:
                    "n_chunks": wl.n_chunks, "n_streams": wl.n_streams,
                    "parallelism": "single GPU, all experts local"},
         "layer_us": ms_per_step * 1e3,
+        "layer_us_stats": step_stats,
         "layer_us_single_pass": ms_single * 1e3,
+        "layer_us_single_pass_stats": single_stats,
+        "gemm_us_stats": stage_stats,
         "layer_us_graph": None if ms_graph is None else ms_graph * 1e3,
         "gemm_tflops": wl.gemm_flop / (gemm_ms / 1e3) / 1e12,
         "gemm_mfma_frac": wl.gemm_flop / (gemm_ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS,
@@ -303,7 +353,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(data, wl, args.cpu_budget)
         n_rows = min(wl.T, 1024) * wl.top_k
-        D_sample = runner.D[:n_rows].view(torch.int16).cpu().numpy().view("uint16")
+        D_sample = runner.D[:n_rows].cpu()
         result["cpu_baseline"]["stages"] = cpu_stage_times(data, wl, D_sample, bm)
     print(json.dumps(result), flush=True)
     return 0
