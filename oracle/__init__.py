@@ -77,7 +77,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_dequant_block128.argtypes = [P, P, i64, i64, i64, P]
     L.oracle_moe_align.argtypes = [P, i64, i32, i32, P, P, P, i64]
     L.oracle_moe_align.restype = ctypes.c_int
-    L.oracle_grouped_gemm.argtypes = [P, P, P, P, P, P, i32, i32, i64, i32, i64, i64, i32, P, P, P]
+    L.oracle_grouped_gemm.argtypes = [P, P, P, P, P, P, i32, i32, i64, i32, i64, i64, i32, P, P, P, P]
     L.oracle_silu_and_mul.argtypes = [P, i64, i64, P]
     L.oracle_moe_reduce.argtypes = [P, i64, i32, i64, P]
     L.oracle_fp8_dequant_sum.argtypes = [P, P, i64, i64, i64, i64, P, i64]
@@ -194,11 +194,12 @@ def moe_align(topk_ids: np.ndarray, E: int, BM: int, max_padded: int | None = No
 
 
 def grouped_gemm(A, a_s, B, b_s, sorted_ids, expert_ids, ntpp, BM, S, top_k,
-                 a_row_by_pos=False, topk_w=None, with_magnitude=False):
+                 a_row_by_pos=False, topk_w=None, with_magnitude=False, with_f32=False):
     """A5/A8: block-scaled FP8 grouped GEMM -> bf16 bits [S, N] (rows by slot;
     rows of slots never placed stay 0).  Reference: overlap/kernels.py:95-214.
     With ``with_magnitude`` also returns fp32 [S, N] L1 magnitudes
-    |w| * sum_kb sum_k |a*b| * a_s * b_s (see moe_oracle.c)."""
+    |w| * sum_kb sum_k |a*b| * a_s * b_s (see moe_oracle.c); with
+    ``with_f32`` also the fp32 results before the bf16 rounding (last)."""
     A = _c(A, np.uint8)
     a_s = _c(a_s, np.float32)
     B = _c(B, np.uint8)
@@ -209,10 +210,12 @@ def grouped_gemm(A, a_s, B, b_s, sorted_ids, expert_ids, ntpp, BM, S, top_k,
     out = np.zeros((S, N), np.uint16)
     mag = np.zeros((S, N), np.float32) if with_magnitude else None
     w = None if topk_w is None else _c(topk_w, np.float32).ravel()
+    f32 = np.zeros((S, N), np.float32) if with_f32 else None
     lib().oracle_grouped_gemm(_ptr(A), _ptr(a_s), _ptr(B), _ptr(b_s), _ptr(sorted_ids),
                               _ptr(expert_ids), int(ntpp), BM, S, top_k, N, K,
-                              1 if a_row_by_pos else 0, _ptr(w), _ptr(out), _ptr(mag))
-    return (out, mag) if with_magnitude else out
+                              1 if a_row_by_pos else 0, _ptr(w), _ptr(out), _ptr(mag), _ptr(f32))
+    res = (out,) + ((mag,) if with_magnitude else ()) + ((f32,) if with_f32 else ())
+    return res if len(res) > 1 else out
 
 
 # Reduced-precision accumulation inside one FP8 MFMA 128-element dot: the
@@ -268,21 +271,23 @@ def moe_layer_stages(x_bf16, topk_ids, topk_w, w13_q, w13_s, w2_q, w2_s, BM):
     rounding points (overlap/overlap_forward.py:153-313):
     quant -> align -> W13 (bf16 C) -> silu_and_mul (bf16 h) -> quant ->
     W2 with routed weight (bf16 D) -> top-k sum (bf16 y).
-    Returns a dict of every intermediate (slot-indexed)."""
+    Returns a dict of every intermediate (slot-indexed), plus the W13 result
+    before its bf16 rounding (c13_f32) and its L1 magnitudes (mag13)."""
     T, H = x_bf16.shape
     k = topk_ids.shape[1]
     E = w13_q.shape[0]
     S = T * k
     q1, s1 = quant_group128(x_bf16)
     sorted_ids, eids, ntpp = moe_align(topk_ids, E, BM)
-    c13 = grouped_gemm(q1, s1, w13_q, w13_s, sorted_ids, eids, ntpp, BM, S, k)
+    c13, mag13, c13_f32 = grouped_gemm(q1, s1, w13_q, w13_s, sorted_ids, eids, ntpp, BM, S, k,
+                                       with_magnitude=True, with_f32=True)
     h = silu_and_mul(c13)
     q2, s2 = quant_group128(h)
     D = grouped_gemm(q2, s2, w2_q, w2_s, sorted_ids, eids, ntpp, BM, S, 1,
                      topk_w=np.ascontiguousarray(topk_w, np.float32).ravel())
     y = moe_reduce(D, T, k)
     return dict(q1=q1, s1=s1, sorted_ids=sorted_ids, expert_ids=eids, ntpp=ntpp,
-                c13=c13, h=h, q2=q2, s2=s2, D=D, y=y)
+                c13=c13, c13_f32=c13_f32, mag13=mag13, h=h, q2=q2, s2=s2, D=D, y=y)
 
 
 # --------------------------------------------------------------------------

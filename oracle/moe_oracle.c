@@ -242,7 +242,7 @@ void oracle_grouped_gemm(const uint8_t* A, const float* a_s, const uint8_t* B,
                          const int32_t* expert_ids, int32_t ntpp, int32_t BM,
                          int64_t S, int32_t top_k, int64_t N, int64_t K,
                          int32_t a_row_by_pos, const float* topk_w,
-                         uint16_t* out, float* mag) {
+                         uint16_t* out, float* mag, float* out_f32) {
     int64_t KB = (K + 127) / 128, NB = (N + 127) / 128;
     float lut[256];
     for (int i = 0; i < 256; ++i) lut[i] = oracle_e4m3_to_f32((uint8_t)i);
@@ -276,6 +276,7 @@ void oracle_grouped_gemm(const uint8_t* A, const float* a_s, const uint8_t* B,
                 l1 *= fabs((double)topk_w[s]);
             }
             out[s * N + n] = oracle_f32_to_bf16(acc);
+            if (out_f32) out_f32[s * N + n] = acc;
             if (mag) mag[s * N + n] = (float)l1;
         }
     }

@@ -163,3 +163,17 @@ def test_reduce_is_fp32_sum_rounded_once():
         acc = acc + Df[:, i]
     ref = torch.from_numpy(acc).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got, ref)
+
+
+def test_grouped_gemm_f32_output_rounds_to_the_bf16_output():
+    """The unrounded fp32 result the oracle can return is the value its bf16
+    output rounds from (every placed slot), and unplaced rows stay zero."""
+    from moe_cases import make_case
+    c = make_case(40, 256, 256, 4, 2, 16, seed=3)
+    q1, s1 = oracle.quant_group128(c.x)
+    srt, eids, ntpp = oracle.moe_align(c.topk_ids, 4, 16)
+    out, mag, f32 = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, srt, eids, ntpp, 16, c.S, 2,
+                                        with_magnitude=True, with_f32=True)
+    assert np.array_equal(oracle.f32_to_bf16(f32), out)
+    assert np.any(f32 != 0) and np.all(np.abs(f32) <= mag * (1 + 1e-6) + 1e-30)
+    assert np.array_equal(oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, srt, eids, ntpp, 16, c.S, 2), out)
