@@ -66,6 +66,20 @@ int moe_align_block_size(const int32_t* topk_ids, int64_t S, int32_t E, int32_t 
                          int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
                          int64_t max_padded, void* workspace, void* stream);
 
+/* A3 without caller memory.  No counterpart in the reference: for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same outputs as moe_align_block_size;
+ * the workspace is a static device array of MOE_ALIGN_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends, so moe_align_workspace_bytes(S, E)
+ * must not exceed it (else MOE_ERR_CAPACITY; DeepSeek-V3's S = 65536, E = 256
+ * needs 0.33 MiB).  Calls that overlap on one GPU share the array and race.
+ * The first call on a device looks the array's address up on that device,
+ * which must be current. */
+#define MOE_ALIGN_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
+int moe_align_block_size_noalloc(const int32_t* topk_ids, int64_t S, int32_t E, int32_t block_size_m,
+                                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
+                                 int64_t max_padded, void* stream);
+
 /* A3 with an expert map (expert parallelism) -- vLLM moe_align_block_size(
  * topk_ids, BM, E, expert_map) as called at overlap/overlap_forward.py:165-169
  * and schemes/vllm_ep.py:57-66: the sort and padding run over the E global

@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "moe_align_workspace_bytes": (ctypes.c_int64, [_i64, _i32]),
     "moe_align_block_size": (ctypes.c_int, [_P, _i64, _i32, _i32, _P, _P, _P, _i64, _P, _P]),
     "moe_align_block_size_mapped": (ctypes.c_int, [_P, _i64, _i32, _i32, _P, _P, _P, _P, _i64, _P, _P]),
+    "moe_align_block_size_noalloc": (ctypes.c_int, [_P, _i64, _i32, _i32, _P, _P, _P, _i64, _P]),
     "moe_grouped_gemm": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32, _i64,
                                         _i64, _i32, _i32, _i64, _P, _P]),
     "moe_grouped_gemm_ordered": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i32,

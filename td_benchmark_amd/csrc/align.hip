@@ -27,6 +27,8 @@
 //      every block (the expert of a position comes from a binary search over
 //      the offsets held in LDS).
 // Align moves well under 2 MB at every configuration, so it is latency-bound.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace moe {
@@ -381,4 +383,51 @@ extern "C" int moe_align_block_size_mapped(const int32_t* topk_ids, int64_t S, i
   if (!expert_map) return kErrNullPointer;
   return align_impl(topk_ids, S, E, BM, expert_map, sorted_ids, expert_ids, ntpp, max_padded, workspace,
                     stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free align: the same three kernels with their workspace in a
+// file-scope device array instead of caller memory, for callers that cannot
+// allocate (code under graph capture, tight serving loops).  Each GPU holds
+// its own copy of the array until the process ends; every call on a GPU
+// shares it, so calls that overlap on one GPU race.  Nothing in the workspace
+// needs clearing: every call writes each chunk count, rank, offset and count
+// that it later reads.
+
+namespace moe {
+
+constexpr int64_t kNoAllocScratchBytes = MOE_ALIGN_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// The array's device address on the current GPU, looked up once per device
+// with that device current (the host-side name is only a stand-in).
+static int scratch_for_current_device(void** out) {
+  static std::mutex mu;
+  static void* ptr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kErrLaunch;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return kErrLaunch;
+    ptr[dev] = p;
+  }
+  *out = ptr[dev];
+  return kOk;
+}
+
+}  // namespace moe
+
+extern "C" int moe_align_block_size_noalloc(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
+                                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
+                                            int64_t max_padded, void* stream) {
+  const int64_t need = moe_align_workspace_bytes(S, E);
+  if (need < 0) return S < 0 ? kErrBadShape : kErrBadExperts;
+  if (need > kNoAllocScratchBytes) return kErrCapacity;
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc != kOk) return rc;
+  return align_impl(topk_ids, S, E, BM, nullptr, sorted_ids, expert_ids, ntpp, max_padded, ws, stream);
 }

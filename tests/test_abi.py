@@ -117,3 +117,19 @@ def test_chunked_and_mapped_entry_points_validate_arguments(L):
     # tile order out of range
     assert L.moe_grouped_gemm_ordered(d, d, d, d, d, d, d, None, 10, 2, 0, 256, 256, 4, 64, 100, 3, d,
                                       None) == E["MOE_ERR_BAD_SHAPE"]
+
+
+def test_noalloc_align_checks_its_limit_before_any_device_call(L):
+    """The allocation-free align rejects a problem whose workspace exceeds its
+    static array (MOE_ALIGN_NOALLOC_SCRATCH_BYTES) and bad sizes before it
+    touches a device, so these calls are safe without a GPU."""
+    text = HEADER.read_text()
+    limit = int(eval(re.search(r"#define\s+MOE_ALIGN_NOALLOC_SCRATCH_BYTES\s+(\([^)]*\))", text).group(1)))
+    assert limit == 4 * 1024 * 1024
+    S, E = 1 << 20, 1024
+    assert L.moe_align_workspace_bytes(S, E) > limit
+    p = ctypes.c_void_p(16)
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, S, E, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_CAPACITY"
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, -1, E, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_BAD_SHAPE"
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, 64, 0, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_BAD_EXPERTS"
+
