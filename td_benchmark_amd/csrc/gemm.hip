@@ -47,6 +47,12 @@
 // they are laid out K-major by sorted position (as_pos_ld) -- one contiguous
 // run of the tile's rows per K block.
 //
+// The MFMA takes the weight fragment as its first operand and the activation
+// fragment as its second, so the four results of a lane are four consecutive
+// columns of one token: a K step needs one scale product a_s * b_s per 16-row
+// subtile and group (not one per row), and the epilogue stages a lane's
+// results with one 4- or 8-byte LDS write.
+//
 // LDS rows are 128 B; the 16 B chunk index of a row is XORed with
 // swz(row) = (row mod 8) ^ bit3(row), which depends only on the row's
 // position inside its 16-row MFMA subtile.  A fragment read (lane = row fr,
@@ -224,11 +230,16 @@ MOE_DEVICE void groups_of(const GemmArgs& g, int64_t j, int64_t& g0, int64_t& g1
   }
 }
 
-// The epilogue of one tile, shared by both K-loop bodies: SiLU*up and the
+// The epilogue of one tile, shared by every tile height: SiLU*up and the
 // 1x128 quant of h written by sorted position (fused W13), or the bf16 rows
 // (routed weights applied) written by slot.  `staging` is LDS for BM x 512 B.
-// Output element (r, gg, c, v) of a lane: row = row_base + r*16 + 4*kseg + v,
-// column (within group gg) = col_base + c*16 + fr.
+// Output element (r, gg, c, v) of a lane: token row = row_base + r*16 + fr,
+// column (within group gg) = col_base + c*16 + 4*kseg + v -- the MFMA takes
+// the weight fragment first, so a lane holds four consecutive columns of one
+// token and stages them with one 4-byte (codes) or 8-byte (bf16) LDS write.
+// Staging rows XOR their 16-byte chunk index with the row (mod 8 for codes,
+// mod 16 for bf16), so the 16 tokens a write instruction covers hit distinct
+// bank groups.
 template <int BM, bool FUSED>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile<BM>::RS][2][Tile<BM>::CS],
                                               int64_t j, int64_t pos0, int rows_avail, int64_t g0,
@@ -245,11 +256,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
   const int fr = lane & 15;
   const int kseg = lane >> 4;
   if constexpr (FUSED) {
-    float pmax[T::RS][4];
+    float pmax[T::RS];
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) pmax[r][v] = 0.0f;
+    for (int r = 0; r < T::RS; ++r) pmax[r] = 0.0f;
 #pragma unroll
     for (int r = 0; r < T::RS; ++r)
 #pragma unroll
@@ -259,66 +268,64 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
           const uint32_t gu = pack_bf16x2(acc[r][0][c][v], acc[r][1][c][v]);
           const float h = silu_mul_bf16(lo_bf16(gu), hi_bf16(gu));
           acc[r][0][c][v] = h;
-          pmax[r][v] = fmaxf(pmax[r][v], fabsf(h));
+          pmax[r] = fmaxf(pmax[r], fabsf(h));
         }
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float m = pmax[r][v];
-        m = fmaxf(m, __shfl_xor(m, 1));
-        m = fmaxf(m, __shfl_xor(m, 2));
-        m = fmaxf(m, __shfl_xor(m, 4));
-        m = fmaxf(m, __shfl_xor(m, 8));
-        if (fr == 0) smRed[wn * BM + row_base + r * 16 + 4 * kseg + v] = m;
-      }
+    for (int r = 0; r < T::RS; ++r) {
+      float m = pmax[r];
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if (kseg == 0) smRed[wn * BM + row_base + r * 16 + fr] = m;
+    }
     __syncthreads();
     uint8_t* stage_out = staging;  // [BM][128] fp8 codes
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r)
+    for (int r = 0; r < T::RS; ++r) {
+      const int row = row_base + r * 16 + fr;
+      float amax = 0.0f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = row_base + r * 16 + 4 * kseg + v;
-        float amax = 0.0f;
+      for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
+      const float sc = group_scale(amax);
+      const float inv = 1.0f / sc;
+      if (wn == 0 && kseg == 0 && row < rows_avail) *hs_at(g, pos0 + row, j) = sc;
 #pragma unroll
-        for (int w = 0; w < T::WN; ++w) amax = fmaxf(amax, smRed[w * BM + row]);
-        const float sc = group_scale(amax);
-        const float inv = 1.0f / sc;
-        if (wn == 0 && fr == 0 && row < rows_avail) *hs_at(g, pos0 + row, j) = sc;
-#pragma unroll
-        for (int c = 0; c < T::CS; c += 2) {
-          const float q0 = clamp_fp8(div_by(acc[r][0][c][v], sc, inv));
-          const float q1 = clamp_fp8(div_by(acc[r][0][c + 1][v], sc, inv));
-          const uint32_t pk = pack4_e4m3(q0, q1, 0.0f, 0.0f);
-          stage_out[row * 128 + col_base + c * 16 + fr] = (uint8_t)(pk & 0xFF);
-          stage_out[row * 128 + col_base + (c + 1) * 16 + fr] = (uint8_t)((pk >> 8) & 0xFF);
-        }
+      for (int c = 0; c < T::CS; ++c) {
+        const float q0 = clamp_fp8(div_by(acc[r][0][c][0], sc, inv));
+        const float q1 = clamp_fp8(div_by(acc[r][0][c][1], sc, inv));
+        const float q2 = clamp_fp8(div_by(acc[r][0][c][2], sc, inv));
+        const float q3 = clamp_fp8(div_by(acc[r][0][c][3], sc, inv));
+        const int col = col_base + c * 16 + 4 * kseg;
+        *reinterpret_cast<uint32_t*>(stage_out + row * 128 + ((((col >> 4) ^ (row & 7)) << 4) | (col & 15))) =
+            pack4_e4m3(q0, q1, q2, q3);
       }
+    }
     __syncthreads();
     for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
       const int row = ci >> 3, cc = ci & 7;
       *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) =
-          *reinterpret_cast<const v4i*>(stage_out + row * 128 + cc * 16);
+          *reinterpret_cast<const v4i*>(stage_out + row * 128 + ((cc ^ (row & 7)) << 4));
     }
   } else {
     // Both 128-column groups staged at once as [BM][256] bf16, then each row's
     // chunks (up to 512 B) written by slot.
     uint16_t* stage_out = reinterpret_cast<uint16_t*>(staging);
 #pragma unroll
-    for (int r = 0; r < T::RS; ++r)
+    for (int r = 0; r < T::RS; ++r) {
+      const int row = row_base + r * 16 + fr;
+      const float w = smW[row];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = row_base + r * 16 + 4 * kseg + v;
-        const float w = smW[row];
+      for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
-        for (int gg = 0; gg < 2; ++gg)
-#pragma unroll
-          for (int c = 0; c < T::CS; ++c) {
-            float val = acc[r][gg][c][v];
-            if (g.topk_w) val = val * w;
-            stage_out[row * 256 + gg * 128 + col_base + c * 16 + fr] = (uint16_t)(pack_bf16x2(val, 0.0f) & 0xFFFFu);
-          }
-      }
+        for (int c = 0; c < T::CS; ++c) {
+          v4f val = acc[r][gg][c];
+          if (g.topk_w) val = val * w;
+          const int col = gg * 128 + col_base + c * 16 + 4 * kseg;  // bf16 column
+          v2u pk;
+          pk[0] = pack_bf16x2(val[0], val[1]);
+          pk[1] = pack_bf16x2(val[2], val[3]);
+          *reinterpret_cast<v2u*>(stage_out + row * 256 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)) = pk;
+        }
+    }
     __syncthreads();
     const int nchunks = g1_store ? 32 : 16;  // 16 B chunks of a row to store
     for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
@@ -326,7 +333,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
       if (cc >= nchunks) continue;
       const int64_t slot = smSlot[row];
       if (slot >= g.S) continue;
-      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + cc * 8);
+      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + ((cc ^ (row & 15)) << 3));
       const int64_t n = (cc < 16 ? g0 : g1) * 128 + (cc & 15) * 8;
       v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
       if (g.accumulate) {
@@ -475,7 +482,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   const int b_lane0 = T::A_BYTES + col_base * 128 + lane0;
   const int b_lane1 = T::A_BYTES + col_base * 128 + lane1;
   const float* smSA = reinterpret_cast<const float*>(smem + T::OFF_SA);
-  const int sa_lane = row_base + 4 * kseg;
+  const int sa_lane = row_base + fr;  // the lane's token (the MFMA's second operand)
 
   issue_stage(0, 0, bg0, bg1);
 #pragma unroll
@@ -518,41 +525,33 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         [&]<int... R>(std::integer_sequence<int, R...>) {
           ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
         }(std::make_integer_sequence<int, RA>{});
-        // Column fragments triple-buffered (two LDS reads in flight ahead of the
-        // MFMAs that use them); MFMA t is issued before the scale
-        // FMAs of MFMA t-kScaleLag, whose result is ready by then.  The per-row
-        // scale products a_s*b_s are formed per group; the MFMAs of the first
-        // group still pending at the group switch (its last kScaleLag, rows
-        // RA-1, RA-2, ...) keep their old products in sab_prev.
+        // Weight fragments triple-buffered (two LDS reads in flight ahead of the
+        // MFMAs that use them); MFMA t is issued before the scale FMAs of MFMA
+        // t - kScaleLag, whose result is ready by then.  The MFMA takes the
+        // weight fragment first, so a lane's four results are four columns of
+        // one token: one scale product a_s * b_s per 16-row subtile and group.
         constexpr int LG = kScaleLag;
-        constexpr int NQ = 2 * T::CS;  // column fragments per step
+        constexpr int NQ = 2 * T::CS;  // weight fragments per step
         constexpr int NT = NQ * RA;
         constexpr int NBQ = 3;
         v8i bq[NBQ];
         v4f p[LG + 1];
-        float sab[RA][4];
-        float sab_prev[LG][4];
+        float sab[2][RA];
+        {
+          const float sb0 = smSB[kk];
+          const float sb1 = smSB[kMaxKB + kk];
+#pragma unroll
+          for (int r = 0; r < RA; ++r) {
+            const float sa = tSA[r * 16];
+            sab[0][r] = sa * sb0;
+            sab[1][r] = sa * sb1;
+          }
+        }
         bq[0] = frag_at<0>(pb0, pb1);
         if constexpr (NQ > 1) bq[1] = frag_at<(1 / T::CS * 128 + 1 % T::CS * 16) * 128>(pb0, pb1);
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
           (
               [&] {
-                constexpr int gg = Q / T::CS, c = Q % T::CS;
-                if constexpr (c == 0) {
-                  if constexpr (gg == 1) {
-#pragma unroll
-                    for (int l = 0; l < LG; ++l)
-#pragma unroll
-                      for (int v = 0; v < 4; ++v) sab_prev[l][v] = sab[((RA - 1 - l) % RA + RA) % RA][v];
-                  }
-                  const float sb = smSB[gg * kMaxKB + kk];
-#pragma unroll
-                  for (int r = 0; r < RA; ++r) {
-                    const v4f sa4 = *reinterpret_cast<const v4f*>(tSA + r * 16);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) sab[r][v] = sa4[v] * sb;
-                  }
-                }
                 if constexpr (Q + NBQ - 1 < NQ) {
                   constexpr int gn = (Q + NBQ - 1) / T::CS, cn = (Q + NBQ - 1) % T::CS;
                   bq[(Q + NBQ - 1) % NBQ] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
@@ -560,18 +559,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 #pragma unroll
                 for (int r = 0; r < RA; ++r) {
                   const int t = Q * RA + r;
-                  p[t % (LG + 1)] = mfma_fp8(af[r], bq[Q % NBQ]);
+                  p[t % (LG + 1)] = mfma_fp8(bq[Q % NBQ], af[r]);
                   if (t >= LG) {
                     const int u = t - LG, uq = u / RA, ur = u % RA;
                     const int ug = uq / T::CS, uc = uq % T::CS;
-                    // a first-group MFMA scaled in the second group: the
-                    // (T::CS*RA - 1 - u)-th from the end of the first group
-                    const int pend = T::CS * RA - 1 - u;
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                      const float sc = (ug == gg) ? sab[ur][v] : sab_prev[pend >= 0 && pend < LG ? pend : 0][v];
-                      acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sc, acc[ur][ug][uc][v]);
-                    }
+                    for (int v = 0; v < 4; ++v)
+                      acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sab[ug][ur], acc[ur][ug][uc][v]);
                   }
                 }
               }(),
@@ -584,13 +578,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
                 if constexpr (u >= 0) {
                   constexpr int uq = u / RA, ur = u % RA;
                   constexpr int ug = uq / T::CS, uc = uq % T::CS;
-                  // a first-group MFMA when the step has fewer MFMAs than LG per group
-                  constexpr int pend = T::CS * RA - 1 - u;
 #pragma unroll
-                  for (int v = 0; v < 4; ++v) {
-                    const float sc = ug == 1 ? sab[ur][v] : sab_prev[pend >= 0 && pend < LG ? pend : 0][v];
-                    acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sc, acc[ur][ug][uc][v]);
-                  }
+                  for (int v = 0; v < 4; ++v)
+                    acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sab[ug][ur], acc[ur][ug][uc][v]);
                 }
               }(),
               ...);
