@@ -603,14 +603,37 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 
 }
 
+// A tile of a BM-row launch whose valid rows fit SUB rows, run with the
+// SUB-row body.  Positions [SUB, rows_avail) are padding: the fused outputs
+// there are the zero codes and floor scales an all-zero row quantises to.
+template <int SUB, int BM, bool FUSED>
+__device__ __forceinline__ void short_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
+                                           int nvalid) {
+  static_assert(Tile<SUB>::THREADS == Tile<BM>::THREADS, "same workgroup size");
+  gemm_tile<SUB, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+  if (FUSED) {
+    const int tid = threadIdx.x;
+    for (int ci = SUB * 8 + tid; ci < rows_avail * 8; ci += Tile<BM>::THREADS) {
+      const int row = ci >> 3, cc = ci & 7;
+      *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
+    }
+    for (int row = SUB + tid; row < rows_avail; row += Tile<BM>::THREADS) *hs_at(g, pos0 + row, j) = kScaleFloor;
+  }
+}
+
+// Dynamic LDS of a launch with BM-row tiles (the larger of the bodies it may run).
+template <int BM>
+constexpr int kernel_lds() {
+  return BM == 256 && Tile<128>::LDS_BYTES > Tile<256>::LDS_BYTES ? Tile<128>::LDS_BYTES : Tile<BM>::LDS_BYTES;
+}
+
 template <int BM, bool FUSED>
 __global__ __launch_bounds__(Tile<BM>::THREADS)
 __attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4, Tile<BM>::NW / 4)))
 void grouped_gemm_kernel(GemmArgs g) {
   using T = Tile<BM>;
-  static_assert(BM <= kTailRows || Tile<kTailRows>::LDS_BYTES <= T::LDS_BYTES,
+  static_assert(BM <= kTailRows || Tile<kTailRows>::LDS_BYTES <= kernel_lds<BM>(),
                 "the short body must fit in the launch's LDS");
-  static_assert(BM <= kTailRows || Tile<kTailRows>::THREADS == T::THREADS, "same workgroup size");
   const int tid = threadIdx.x;
 
   // ---- expert-aligned, XCD-aware tile mapping ----------------------------
@@ -736,22 +759,20 @@ void grouped_gemm_kernel(GemmArgs g) {
   bool row_valid = false;
   if (tid < BM && tid < rows_avail) row_valid = g.sorted[pos0 + tid] < g.S;
   const int nvalid = __syncthreads_count(row_valid);
+  // A tile with few valid rows (an expert's last rows, or a one-block tile of
+  // a run split over tiles) runs a shorter body: kTailRows rows, bound by
+  // streaming its weight tile with a three-deep LDS ring; or, in a 256-row
+  // launch, the 128-row body, whose eight waves split the 128 rows into 64 x 64
+  // subtiles instead of leaving half of the 256-row body's MFMAs on padding.
   if constexpr (BM > kTailRows) {
-    // A tile with few valid rows (an expert's last rows) is bound by streaming
-    // its weight tile: it runs with kTailRows-row operand tiles, whose small
-    // stages give a three-deep LDS ring, and a kTailRows-row epilogue.  Rows
-    // past kTailRows are padding; the fused outputs of those positions are the
-    // zero codes and floor scales an all-zero row quantises to.
     if (nvalid <= kTailRows) {
-      gemm_tile<kTailRows, FUSED>(g, j, pos0, rows_avail, e, nvalid);
-      if (FUSED) {
-        for (int ci = kTailRows * 8 + tid; ci < rows_avail * 8; ci += T::THREADS) {
-          const int row = ci >> 3, cc = ci & 7;
-          *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
-        }
-        for (int row = kTailRows + tid; row < rows_avail; row += T::THREADS)
-          *hs_at(g, pos0 + row, j) = kScaleFloor;
-      }
+      short_tile<kTailRows, BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+      return;
+    }
+  }
+  if constexpr (BM == 256) {
+    if (nvalid <= 128) {
+      short_tile<128, BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
       return;
     }
   }
@@ -764,13 +785,13 @@ static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   // Set once per process (a function-local static is initialised exactly once,
   // also when several host threads make their first call together).
   static const hipError_t attr_rc = hipFuncSetAttribute(
-      (const void*)grouped_gemm_kernel<BM, FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+      (const void*)grouped_gemm_kernel<BM, FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, kernel_lds<BM>());
   if (attr_rc != hipSuccess) return kErrLaunch;
   // Upper bound on the tile count (the real one depends on ntpp, on the device).
   const int64_t grid = (args.max_blocks * args.n_tiles + kXcds - 1) / kXcds * kXcds;
   if (grid <= 0) return kOk;
   hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(T::THREADS),
-                     T::LDS_BYTES, st, args);
+                     kernel_lds<BM>(), st, args);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
