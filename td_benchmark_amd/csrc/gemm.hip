@@ -206,11 +206,24 @@ template <int N>
 MOE_DEVICE void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 MOE_DEVICE void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-MOE_DEVICE void dma16(const uint8_t* g, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 16, 0, 0);
+// Direct-to-LDS loads, issued from inline asm.  The compiler's wait-count
+// pass treats its own form of these loads as pending on both the vector-memory
+// and the LDS counters, and while one is in flight it waits for every
+// outstanding LDS read (lgkmcnt 0) at each use of an LDS read, so the fragment
+// reads of a K step could not overlap each other.  The kernel waits for these
+// loads itself (s_waitcnt vmcnt + s_barrier before the stage is read).  M0
+// holds the LDS destination (a wave-uniform byte address), the global address
+// is the uniform 64-bit base plus the lane's 32-bit offset.  M0 is written
+// here only: the kernels that call these use no other M0-based instruction.
+MOE_DEVICE void dma16(const uint8_t* base, uint32_t off, uint8_t* lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+               : "memory");
 }
-MOE_DEVICE void dma4(const uint8_t* g, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(g, MOE_LDS(lds), 4, 0, 0);
+MOE_DEVICE void dma4(const uint8_t* base, uint32_t off, uint8_t* lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m)
+               : "memory");
 }
 
 // Column scale groups of n-tile j: W13 gate group j and up group I/128 + j; the
@@ -446,7 +459,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
       const int gi = wave + T::NW * i;
       uint32_t off = a_off[i];
       asm volatile("" : "+v"(off));
-      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase + off, dst + gi * 1024);
+      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase, off, dst + gi * 1024);
     }
     uint32_t boff = b_off;
     asm volatile("" : "+v"(boff));
@@ -454,12 +467,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 #pragma unroll
     for (int i = 0; i < T::NB_W; ++i) {
       const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
-      dma16(bbase + boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+      dma16(bbase, boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
     }
     if (s_idx < T::NS) {
       uint32_t soff = sa_off;
       asm volatile("" : "+v"(soff));
-      dma4(reinterpret_cast<const uint8_t*>(g.as_pos_ld ? g.As + kk * g.as_pos_ld : g.As + kk) + soff,
+      dma4(reinterpret_cast<const uint8_t*>(g.as_pos_ld ? g.As + kk * g.as_pos_ld : g.As + kk), soff,
            smem + T::OFF_SA + stage * T::NS * 256 + s_idx * 256);
     }
   };
