@@ -204,7 +204,6 @@ MOE_DEVICE v8i frag_at(const uint8_t* base0, const uint8_t* base1) {
 MOE_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 template <int N>
 MOE_DEVICE void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-MOE_DEVICE void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Direct-to-LDS loads, issued from inline asm.  The compiler's wait-count
 // pass treats its own form of these loads as pending on both the vector-memory
@@ -453,14 +452,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   // hoisted and kept live (which exhausts the registers of the 256-row tile).
   auto issue_stage = [&](int kk, int stage, const uint8_t* bg0, const uint8_t* bg1) {
     uint8_t* dst = smem + stage * T::STAGE;
-    const uint8_t* abase = g.A + kk * 128;
-#pragma unroll
-    for (int i = 0; i < T::NA_W; ++i) {
-      const int gi = wave + T::NW * i;
-      uint32_t off = a_off[i];
-      asm volatile("" : "+v"(off));
-      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase, off, dst + gi * 1024);
-    }
+    // Weight rows first: they come from HBM, the A rows mostly from L2.
     uint32_t boff = b_off;
     asm volatile("" : "+v"(boff));
     constexpr int HALF = T::NB_W / 2;
@@ -468,6 +460,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     for (int i = 0; i < T::NB_W; ++i) {
       const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
       dma16(bbase, boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+    }
+    const uint8_t* abase = g.A + kk * 128;
+#pragma unroll
+    for (int i = 0; i < T::NA_W; ++i) {
+      const int gi = wave + T::NW * i;
+      uint32_t off = a_off[i];
+      asm volatile("" : "+v"(off));
+      if (gi < T::NA && 8 * gi < a_rows_needed) dma16(abase, off, dst + gi * 1024);
     }
     if (s_idx < T::NS) {
       uint32_t soff = sa_off;
@@ -477,12 +477,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     }
   };
 
-  // Weight scales of both groups for every K block (2*KB <= 256 <= THREADS:
-  // one per thread), loaded before the first stages are issued and stored to
-  // LDS after them, so their latency overlaps the first DMA.
-  static_assert(2 * kMaxKB <= T::THREADS, "one weight scale per thread");
-  float sb_val = 0.0f;
-  if (tid < 2 * KB) sb_val = bs_expert[(tid < KB ? g0 : g1) * g.bs_ld + tid % KB];
+  // Weight scales of both groups for every K block, smSB[g * kMaxKB + kk]:
+  // one 4-byte direct-to-LDS load per lane of waves 0-3 (entry 64 * wave +
+  // lane), issued before stage 0, so that step 0's wait covers them.  Entries
+  // past KB read a valid scale and are never used.
+  static_assert(2 * kMaxKB == 4 * 64 && Tile<BM>::NW >= 4, "four waves load the weight scales");
+  auto issue_weight_scales = [&] {
+    if (wave < 4) {
+      const int idx = 64 * wave + lane;
+      const int kb = idx % kMaxKB;
+      const int64_t grp = idx < kMaxKB ? g0 : g1;
+      uint32_t off = (uint32_t)((grp * g.bs_ld + (kb < KB ? kb : 0)) * 4);
+      asm volatile("" : "+v"(off));
+      dma4(reinterpret_cast<const uint8_t*>(bs_expert), off, reinterpret_cast<uint8_t*>(smSB) + 256 * wave);
+    }
+  };
 
   const int row_base = wm * T::RS * 16;
   const int col_base = wn * T::CS * 16;
@@ -497,12 +506,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
   const float* smSA = reinterpret_cast<const float*>(smem + T::OFF_SA);
   const int sa_lane = row_base + fr;  // the lane's token (the MFMA's second operand)
 
+  issue_weight_scales();
   issue_stage(0, 0, bg0, bg1);
 #pragma unroll
   for (int st = 1; st < T::KS - 1; ++st)
     if (st < KB) issue_stage(st, st, bg0, bg1);
-  if (tid < 2 * KB) smSB[(tid / KB) * kMaxKB + tid % KB] = sb_val;
-  wait_lgkm0();  // the weight-scale ds_writes
 
   int ra = (nvalid - row_base + 15) / 16;
   ra = ra < 0 ? 0 : (ra > T::RS ? T::RS : ra);
@@ -526,7 +534,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
       else wait_vmcnt<0>();
       block_barrier();
       // The buffer read at step kk-1 is free once every wave has passed the barrier.
+      // The waves issue the stage's loads at raised priority, so that all of
+      // them are in flight before the MFMAs of any wave take the issue slots.
+      __builtin_amdgcn_s_setprio(3);
       if (kk + T::KS - 1 < KB) issue_stage(kk + T::KS - 1, stage == 0 ? T::KS - 1 : stage - 1, bg0, bg1);
+      __builtin_amdgcn_s_setprio(0);
       if constexpr (RA > 0) {
         const uint8_t* st = smem + stage * T::STAGE;
         const uint8_t* pa0 = st + a_lane0;

@@ -91,3 +91,24 @@ def test_microbench_sweeps_match_reference():
     assert mb_dispatch_prep.SWEEP["M"] == [1024, 2048, 4096, 6647]
     assert len(list(iter_cases(mb_moe_align.SWEEP, 0))) == 16
     assert len(list(iter_cases(mb_moe_align.SWEEP, 3))) == 3
+
+
+def test_tile_order_l2_hit_rate_reads_rocprof_counter_rows(tmp_path):
+    """The l2_hit_rate of the tile-order microbench: TCC hits over hits plus
+    misses, summed over the grouped GEMM's dispatches only."""
+    from td_benchmark_amd.microbench.mb_tile_order_groupgemm import l2_hit_rate_from_csv
+
+    cols = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    rows = [(1, "void moe::grouped_gemm_kernel<64, false>(moe::GemmArgs)", "TCC_HIT_sum", 300.0),
+            (1, "void moe::grouped_gemm_kernel<64, false>(moe::GemmArgs)", "TCC_MISS_sum", 100.0),
+            (2, "void moe::grouped_gemm_kernel<64, false>(moe::GemmArgs)", "TCC_HIT_sum", 500.0),
+            (2, "void moe::grouped_gemm_kernel<64, false>(moe::GemmArgs)", "TCC_MISS_sum", 100.0),
+            (3, "void moe::quant_group128_kernel<false>(...)", "TCC_HIT_sum", 0.0),
+            (3, "void moe::quant_group128_kernel<false>(...)", "TCC_MISS_sum", 1e9)]
+    path = tmp_path / "l2_counter_collection.csv"
+    with path.open("w", newline="") as fh:
+        w = __import__("csv").writer(fh, quoting=__import__("csv").QUOTE_NONNUMERIC)
+        w.writerow(cols)
+        w.writerows(rows)
+    assert l2_hit_rate_from_csv([path]) == 800.0 / 1000.0
+    assert l2_hit_rate_from_csv([path], kernel_substr="no_such_kernel") is None
