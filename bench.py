@@ -78,14 +78,20 @@ def summarize_samples(samples_ms: list[float]) -> dict[str, float]:
 
 
 def cpu_model_name() -> str:
-    """The host CPU's model name as lscpu reports it (/proc/cpuinfo if lscpu
-    is unavailable)."""
+    """The host CPU's model name as lscpu reports it, with its CPU family /
+    model / stepping numbers (a virtualised host may report only a generic
+    name); /proc/cpuinfo if lscpu is unavailable."""
     import subprocess
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = {}
         for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields.setdefault(k.strip(), v.strip())
+        if "Model name" in fields:
+            ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k)]
+            return fields["Model name"] + (f" ({', '.join(ids)})" if ids else "")
     except (OSError, subprocess.SubprocessError):
         pass
     try:
