@@ -291,6 +291,26 @@ def main() -> int:
         torch.cuda.synchronize()
         ms_per_step = start.elapsed_time(end) / args.steps
         step_stats = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in pev])
+    # Config 5 also in the reference pipeline's own compute-stream structure
+    # (W13 K-split into a bf16 C13, SiLU*up, quant, W2 N-split; no comm legs),
+    # reported beside the token-chunk pipeline and the single pass.
+    kn_stats = None
+    if pipe is not None:
+        split = ops.SplitExpertsRunner(data.w13, data.w13_s, data.w2, data.w2_s, wl.T, wl.top_k, wl.n_chunks,
+                                       wl.n_chunks, bm)
+        for _ in range(args.warmup):
+            split.run(data.x, data.topk_w, data.topk_ids)
+        torch.cuda.synchronize()
+        kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for i in range(args.steps):
+            kev[i][0].record()
+            split.run(data.x, data.topk_w, data.topk_ids)
+            kev[i][1].record()
+        torch.cuda.synchronize()
+        kn_stats = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in kev])
+        del split
+        torch.cuda.empty_cache()
 
     ntpp = int(runner.align.ntpp.item())
     counts = torch.bincount(data.topk_ids.view(-1).long(), minlength=wl.E)
@@ -349,6 +369,7 @@ def main() -> int:
         "layer_us_single_pass_stats": single_stats,
         "gemm_us_stats": stage_stats,
         "layer_us_graph": None if ms_graph is None else ms_graph * 1e3,
+        "layer_us_kn_split_stats": kn_stats,
         "gemm_tflops": wl.gemm_flop / (gemm_ms / 1e3) / 1e12,
         "gemm_mfma_frac": wl.gemm_flop / (gemm_ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS,
         "stages": stages,

@@ -854,6 +854,84 @@ class ChunkedExpertsRunner:
         return self.y
 
 
+def _split_bounds(total: int, n: int) -> list[tuple[int, int]]:
+    """``total`` (a multiple of 128) in ``n`` chunks of whole 128-blocks, as
+    even as possible (the first chunks take the extra blocks)."""
+    blocks = total // 128
+    n = max(1, min(n, blocks))
+    sizes = [blocks // n + (1 if c < blocks % n else 0) for c in range(n)]
+    out, k = [], 0
+    for b in sizes:
+        out.append((k * 128, (k + b) * 128))
+        k += b
+    return out
+
+
+class SplitExpertsRunner:
+    """The reference pipeline's compute-stream structure on one device
+    (overlap/overlap_forward.py:252-313 without its all-gather and
+    reduce-scatter legs): W13 as ``n_chunks_gateup`` K-split GEMMs
+    accumulating into a bf16 C13 (``invoke_moe_kernel_k_split``,
+    overlap_forward.py:264-274), ``silu_and_mul`` (:277-279), the 1x128 quant
+    of h (:282-284), W2 as ``n_chunks_down`` N-split GEMMs with routed weights
+    (``invoke_moe_kernel_n_split``, :289-302) and the top-k sum (:304-313).
+    Each weight slice is read once; SiLU*up and the quant cannot be fused into
+    a K-split W13, so C13 [S, 2I] and h [S, I] exist in bf16, and every K
+    chunk after the first re-reads and re-writes C13.
+
+    The activation quant runs once over [T, H]: 1x128 groups never straddle a
+    128-aligned chunk, so the codes and scales equal those of quantising each
+    K chunk separately (the reference quantises each all-gathered chunk).
+    Every buffer is allocated here; ``run`` only launches."""
+
+    def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
+                 w2_scale: torch.Tensor, num_tokens: int, top_k: int, n_chunks_gateup: int = 4,
+                 n_chunks_down: int = 4, block_size_m: int | None = None):
+        E, N2, H = _need_weights(w13, w13_scale, "w13")
+        _need_weights(w2, w2_scale, "w2")
+        if w2.shape != (E, H, N2 // 2):
+            raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+        self.E, self.H, self.I, self.T, self.top_k = E, H, N2 // 2, num_tokens, top_k
+        self.S = num_tokens * top_k
+        self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
+        if self.BM not in SUPPORTED_BLOCK_M:
+            raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
+        self.k_bounds = _split_bounds(H, n_chunks_gateup)
+        self.n_bounds = _split_bounds(H, n_chunks_down)
+        self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
+        dev = w13.device
+        S1 = max(self.S, 1)
+        self.q1 = torch.empty((self.T, H), dtype=FP8, device=dev)
+        self.s1 = torch.empty((self.T, H // 128), dtype=torch.float32, device=dev)
+        self.align = AlignBuffers(self.S, E, self.BM, dev)
+        self.C13 = torch.empty((S1, N2), dtype=torch.bfloat16, device=dev)
+        self.h = torch.empty((S1, self.I), dtype=torch.bfloat16, device=dev)
+        self.hq = torch.empty((S1, self.I), dtype=FP8, device=dev)
+        self.hs = torch.empty((S1, self.I // 128), dtype=torch.float32, device=dev)
+        self.D = torch.empty((S1, H), dtype=torch.bfloat16, device=dev)
+        self.y = torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
+        self.config = {"BLOCK_SIZE_M": self.BM}
+
+    def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
+        _need(hidden, "hidden_states", torch.bfloat16)
+        if tuple(hidden.shape) != (self.T, self.H):
+            raise ValueError(f"hidden_states must be [{self.T}, {self.H}]")
+        per_token_group_quant_fp8(hidden, out_q=self.q1, out_s=self.s1)
+        sorted_ids, eids, ntpp = self.align.run(topk_ids.reshape(-1))
+        for c, (k0, k1) in enumerate(self.k_bounds):
+            invoke_moe_kernel_k_split(self.q1, self.w13, self.C13, self.s1, self.w13_scale, None, sorted_ids, eids,
+                                      ntpp, False, self.top_k, self.config, K_offset=k0, K_chunk=k1 - k0,
+                                      is_first_chunk=(c == 0))
+        silu_and_mul(self.h, self.C13)
+        per_token_group_quant_fp8(self.h, out_q=self.hq, out_s=self.hs)
+        w = topk_weights.reshape(-1)
+        for n0, n1 in self.n_bounds:
+            invoke_moe_kernel_n_split(self.hq, self.w2, self.D, self.hs, self.w2_scale, None, w, sorted_ids, eids,
+                                      ntpp, True, 1, self.config, N_offset=n0, N_chunk=n1 - n0)
+        moe_sum(self.D[: self.S], self.y, self.top_k)
+        return self.y
+
+
 def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                   topk_weights: torch.Tensor, topk_ids: torch.Tensor, global_num_experts: int = -1,
                   w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,

@@ -159,3 +159,17 @@ def test_bench_cpu_baseline_runs_the_torch_golden_on_all_cores():
     D = torch.zeros((wl.S, wl.H), dtype=torch.bfloat16)
     st = bench.cpu_stage_times(data, wl, D, wl.block_m)
     assert st["quant_us"] > 0 and st["align_us"] > 0 and st["reduce_us"] > 0
+
+
+def test_split_bounds_are_whole_128_blocks_covering_the_range():
+    from td_benchmark_amd.ops import _split_bounds
+
+    assert _split_bounds(2048, 4) == [(0, 512), (512, 1024), (1024, 1536), (1536, 2048)]
+    assert _split_bounds(640, 4) == [(0, 256), (256, 384), (384, 512), (512, 640)]
+    assert _split_bounds(256, 4) == [(0, 128), (128, 256)]   # never an empty chunk
+    for total in (128, 384, 7168):
+        for n in (1, 2, 3, 5):
+            b = _split_bounds(total, n)
+            assert b[0][0] == 0 and b[-1][1] == total
+            assert all(k0 < k1 and k0 % 128 == 0 and k1 % 128 == 0 for k0, k1 in b)
+            assert all(b[i][1] == b[i + 1][0] for i in range(len(b) - 1))
