@@ -100,6 +100,27 @@ MOE_DEVICE uint32_t pack4_e4m3(float a, float b, float c, float d) {
   return (uint32_t)w | sg;
 }
 
+// Four values of one 1x128 group with scale s > 0 (inv = RN(1/s)) -> four
+// packed e4m3fn codes, e4m3_RNE(clamp(RN(x / s), +-448)).  The quotient is
+// the correctly rounded one of div_by without its sign copy: a quotient that
+// is zero or rounds to zero in e4m3 gets x's sign from the sign bytes ORed in
+// below (x / s has x's sign, and -0 / s = -0), as torch's cast keeps -0;
+// for every other code the OR is a no-op.  Two v_perm_b32 gather the four
+// sign bytes; bit-identical to pack4_e4m3 of clamp_fp8(div_by(x, s, inv)).
+MOE_DEVICE uint32_t quant4_e4m3(float a, float b, float c, float d, float s, float inv) {
+  auto q = [&](float x) {
+    const float q0 = x * inv;
+    const float r = __builtin_fmaf(-q0, s, x);
+    return clamp_fp8(__builtin_fmaf(r, inv, q0));
+  };
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q(a), q(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q(c), q(d), w, true);
+  // byte 3 of a, b -> bytes 0, 1; byte 3 of c, d -> bytes 2, 3
+  const uint32_t ab = __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0703u);
+  const uint32_t cd = __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x07030c0cu);
+  return (uint32_t)w | ((ab | cd) & 0x80808080u);
+}
+
 // Group scale of verify.py:115: max(amax / 448, 1e-12), IEEE division.
 MOE_DEVICE float group_scale(float amax) {
   float s = amax / kFp8Max;

@@ -302,13 +302,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
       if (wn == 0 && kseg == 0 && row < rows_avail) *hs_at(g, pos0 + row, j) = sc;
 #pragma unroll
       for (int c = 0; c < T::CS; ++c) {
-        const float q0 = clamp_fp8(div_by(acc[r][0][c][0], sc, inv));
-        const float q1 = clamp_fp8(div_by(acc[r][0][c][1], sc, inv));
-        const float q2 = clamp_fp8(div_by(acc[r][0][c][2], sc, inv));
-        const float q3 = clamp_fp8(div_by(acc[r][0][c][3], sc, inv));
         const int col = col_base + c * 16 + 4 * kseg;
         *reinterpret_cast<uint32_t*>(stage_out + row * 128 + ((((col >> 4) ^ (row & 7)) << 4) | (col & 15))) =
-            pack4_e4m3(q0, q1, q2, q3);
+            quant4_e4m3(acc[r][0][c][0], acc[r][0][c][1], acc[r][0][c][2], acc[r][0][c][3], sc, inv);
       }
     }
     __syncthreads();

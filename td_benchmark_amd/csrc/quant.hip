@@ -81,10 +81,8 @@ __global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(
     amax = fmaxf(amax, __shfl_xor(amax, 8));
     const float sc = group_scale(amax);
     const float inv = 1.0f / sc;
-    const uint32_t lo = pack4_e4m3(clamp_fp8(div_by(v[0], sc, inv)), clamp_fp8(div_by(v[1], sc, inv)),
-                                   clamp_fp8(div_by(v[2], sc, inv)), clamp_fp8(div_by(v[3], sc, inv)));
-    const uint32_t hi = pack4_e4m3(clamp_fp8(div_by(v[4], sc, inv)), clamp_fp8(div_by(v[5], sc, inv)),
-                                   clamp_fp8(div_by(v[6], sc, inv)), clamp_fp8(div_by(v[7], sc, inv)));
+    const uint32_t lo = quant4_e4m3(v[0], v[1], v[2], v[3], sc, inv);
+    const uint32_t hi = quant4_e4m3(v[4], v[5], v[6], v[7], sc, inv);
     if (ch < n_chunks) {
       __builtin_nontemporal_store((v2u){lo, hi}, reinterpret_cast<v2u*>(q + ch * 8));
       if ((tid & 15) == 0) s[ch >> 4] = sc;
