@@ -30,7 +30,8 @@
 // accumulator.  The fp32 promotion at every 128-K block also bounds the matrix
 // core's reduced-precision accumulation inside one instruction.  16-row
 // subtiles that hold only padding rows issue no MFMA at all, and a tile with
-// at most kTailRows valid rows runs a kTailRows-row body.
+// at most kTailRows valid rows runs a kTailRows-row body (in a 256-row launch,
+// a tile with at most 128 valid rows runs the 128-row body).
 //
 // Pipeline: operand tiles go to LDS by direct-to-LDS loads
 // (global_load_lds_dwordx4: each lane moves 16 B from its own global address
@@ -45,7 +46,10 @@
 // a valid row are then not fetched.  The activation scales of a stage are one
 // 4-byte direct-to-LDS load per row: from the row's own scale row, or -- when
 // they are laid out K-major by sorted position (as_pos_ld) -- one contiguous
-// run of the tile's rows per K block.
+// run of the tile's rows per K block.  The weight scales of the tile (both
+// groups, every K block) arrive by direct-to-LDS loads before stage 0.  All
+// direct-to-LDS loads are issued from inline asm (see dma16), weight rows
+// before A rows, at raised wave priority.
 //
 // The MFMA takes the weight fragment as its first operand and the activation
 // fragment as its second, so the four results of a lane are four consecutive
