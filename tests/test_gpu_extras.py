@@ -260,7 +260,7 @@ def test_shared_expert_rejects_unprepared_row_counts():
 
 
 @pytest.mark.parametrize("name", ["mb_moe_align", "mb_quant_kernels", "mb_group_gemm",
-                                  "mb_tile_order_groupgemm", "mb_dispatch_prep"])
+                                  "mb_tile_order_groupgemm", "mb_dispatch_prep", "mb_chunk_overlap"])
 def test_microbench_writes_measured_rows(name, tmp_path):
     import importlib
 

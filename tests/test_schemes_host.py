@@ -76,12 +76,12 @@ def test_microbench_exp_ids_match_reference_scripts():
                            capture_output=True, text=True, timeout=120, cwd=ROOT)
         ids[name] = json.loads(r.stdout)["exp_id"]
     assert ids == {"mb_moe_align": "EXP-010", "mb_dispatch_prep": "EXP-011", "mb_tile_order_groupgemm": "EXP-012",
-                   "mb_group_gemm": "EXP-014", "mb_quant_kernels": "EXP-015"}
+                   "mb_group_gemm": "EXP-014", "mb_quant_kernels": "EXP-015", "mb_chunk_overlap": "EXP-016"}
 
 
 def test_microbench_sweeps_match_reference():
-    from td_benchmark_amd.microbench import (mb_dispatch_prep, mb_group_gemm, mb_moe_align, mb_quant_kernels,
-                                             mb_tile_order_groupgemm)
+    from td_benchmark_amd.microbench import (mb_chunk_overlap, mb_dispatch_prep, mb_group_gemm, mb_moe_align,
+                                             mb_quant_kernels, mb_tile_order_groupgemm)
     from td_benchmark_amd.microbench.common import iter_cases
 
     assert mb_moe_align.SWEEP == {"M": [1024, 2048, 4096, 6647], "E": [64, 128], "top_k": [8, 16]}
@@ -89,6 +89,9 @@ def test_microbench_sweeps_match_reference():
     assert mb_group_gemm.SWEEP["tile"] == [64, 128, 256]
     assert mb_tile_order_groupgemm.SWEEP["order"] == ["expert_major", "phase_major", "half_phase"]
     assert mb_dispatch_prep.SWEEP["M"] == [1024, 2048, 4096, 6647]
+    # microbench/mb_chunk_overlap.py sweep, with M of REWORK-B.md:960
+    assert mb_chunk_overlap.SWEEP == {"M": [1024, 5120], "scheme": ["b1", "b2", "b3"],
+                                      "n_chunks": [1, 2, 4, 8, 16]}
     assert len(list(iter_cases(mb_moe_align.SWEEP, 0))) == 16
     assert len(list(iter_cases(mb_moe_align.SWEEP, 3))) == 3
 
