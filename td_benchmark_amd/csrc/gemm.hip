@@ -957,6 +957,8 @@ static int setup_plain(GemmArgs& g, int& TM, const void* A, const float* A_scale
   if (E <= 0) return kErrBadExperts;
   if (!block_m_ok(BM)) return kErrBadBlockSize;
   TM = resolve_tile_m(0, BM, S, E);
+  // nothing to compute: the caller returns before touching g (empty operands may be null)
+  if (max_padded == 0 || S == 0) return kOk;
   if (!A || !A_scale || !B || !B_scale || !sorted_ids || !expert_ids || !ntpp || !C)
     return kErrNullPointer;
   g = GemmArgs{};

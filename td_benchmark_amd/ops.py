@@ -916,6 +916,8 @@ class SplitExpertsRunner:
         _need(hidden, "hidden_states", torch.bfloat16)
         if tuple(hidden.shape) != (self.T, self.H):
             raise ValueError(f"hidden_states must be [{self.T}, {self.H}]")
+        if self.S == 0:
+            return self.y  # no tokens: [0, H]
         per_token_group_quant_fp8(hidden, out_q=self.q1, out_s=self.s1)
         sorted_ids, eids, ntpp = self.align.run(topk_ids.reshape(-1))
         for c, (k0, k1) in enumerate(self.k_bounds):
