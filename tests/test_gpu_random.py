@@ -1,0 +1,150 @@
+"""GPU: randomised parity of the grouped GEMM (A5, A8) and the whole layer
+(A1 -> A9) against the oracle, through the C ABI.
+
+Hypothesis (derandomised, so every run draws the same cases) picks the token
+count, hidden and intermediate widths (whole 128-blocks), expert count, top-k,
+align block size, workgroup tile height and a routing with a hot expert, then:
+
+* the plain W13 GEMM (A rows by token, overlap_forward.py:261-274) and the
+  routed W2 GEMM (A rows by sorted position, routed weight in the epilogue,
+  overlap_forward.py:289-302) on random FP8 codes and scales must stay within
+  the GEMM bound of the oracle (1 bf16 ulp plus the FP8 MFMA's accumulation
+  bound; overlap/kernels.py:95-214);
+* the layer must pass the reference worker's three gates and the calibrated
+  bound against the fp8-sim golden (verify.py:14-47, worker.py:107-110) and
+  max-abs-rel 2e-2 against the fp32 reference on the dequantised operands it
+  consumed.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+import oracle
+from moe_cases import bf16_bits, dequant_weights_f32, make_case, to_gpu, u8_bits
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def _fp8_codes(rng, shape):
+    q = rng.integers(0, 256, size=shape, dtype=np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0  # no NaN codes
+    return q
+
+
+@st.composite
+def gemm_cases(draw):
+    E = draw(st.integers(1, 24))
+    k = draw(st.integers(1, min(8, E)))
+    T = draw(st.integers(1, 200))
+    H = 128 * draw(st.integers(1, 4))
+    I = 128 * draw(st.integers(1, 3))
+    BM = draw(st.sampled_from([16, 32, 64, 128]))
+    tile_m = draw(st.sampled_from([0] + [t for t in (16, 32, 64, 128, 256) if t >= BM]))
+    hot = draw(st.integers(0, E - 1))
+    skew = draw(st.floats(0.0, 0.9))
+    seed = draw(st.integers(0, 2**31 - 1))
+    return dict(T=T, H=H, I=I, E=E, k=k, BM=BM, tile_m=tile_m, hot=hot, skew=skew, seed=seed)
+
+
+def _routing(case, rng):
+    T, E, k = case["T"], case["E"], case["k"]
+    ids = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    ids[rng.random((T, k)) < case["skew"]] = case["hot"]
+    w = rng.random((T, k), dtype=np.float32) + np.float32(0.05)
+    return ids, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def _gpu(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.view(dtype) if dtype is not None else t
+
+
+@settings(max_examples=60, deadline=None, derandomize=True)
+@given(gemm_cases())
+def test_random_w13_plain_and_w2_routed_gemms_within_the_bound(case):
+    from td_benchmark_amd import ops
+
+    print(f"case: random gemm {case}", flush=True)
+    rng = np.random.default_rng(case["seed"])
+    T, H, I, E, k, BM, tm = (case[x] for x in ("T", "H", "I", "E", "k", "BM", "tile_m"))
+    S = T * k
+    ids, w = _routing(case, rng)
+    x = oracle.f32_to_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    q1, s1 = oracle.quant_group128(x)
+    w13 = _fp8_codes(rng, (E, 2 * I, H))
+    w13_s = (rng.random((E, 2 * I // 128, H // 128), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    w2 = _fp8_codes(rng, (E, H, I))
+    w2_s = (rng.random((E, H // 128, I // 128), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    srt, eids, ntpp = oracle.moe_align(ids, E, BM)
+    d_srt, d_eids = _gpu(srt), _gpu(eids)
+    d_ntpp = torch.tensor([ntpp], dtype=torch.int32, device="cuda")
+    cfg = {"BLOCK_SIZE_M": BM}
+
+    # W13, plain epilogue, A rows by token
+    ref, mag = oracle.grouped_gemm(q1, s1, w13, w13_s, srt, eids, ntpp, BM, S, k, with_magnitude=True)
+    C = torch.zeros((T, k, 2 * I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(_gpu(q1, torch.float8_e4m3fn), _gpu(w13, torch.float8_e4m3fn), C, _gpu(s1),
+                                  _gpu(w13_s), None, None, d_srt, d_eids, d_ntpp, False, k, cfg, tile_m=tm)
+    torch.cuda.synchronize()
+    bad = oracle.gemm_close(bf16_bits(C).reshape(S, 2 * I), ref, mag)
+    assert not bad.any(), f"W13: {int(bad.sum())} of {bad.size} outside the bound"
+
+    # W2, A rows by sorted position, routed weights
+    mp = srt.size
+    hq = _fp8_codes(rng, (mp, I))
+    hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
+    ref2, mag2 = oracle.grouped_gemm(hq, hs, w2, w2_s, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
+                                     topk_w=w.ravel(), with_magnitude=True)
+    D = torch.zeros((S, 1, H), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(_gpu(hq, torch.float8_e4m3fn), _gpu(w2, torch.float8_e4m3fn), D, _gpu(hs),
+                                  _gpu(w2_s), None, _gpu(w.ravel()), d_srt, d_eids, d_ntpp, True, 1, cfg,
+                                  a_by_pos=True, tile_m=tm)
+    torch.cuda.synchronize()
+    bad = oracle.gemm_close(bf16_bits(D).reshape(S, H), ref2, mag2)
+    assert not bad.any(), f"W2: {int(bad.sum())} of {bad.size} outside the bound"
+
+
+@st.composite
+def layer_cases(draw):
+    E = draw(st.integers(1, 32))
+    return dict(T=draw(st.integers(1, 160)), H=128 * draw(st.integers(1, 4)), I=128 * draw(st.integers(1, 3)),
+                E=E, k=draw(st.integers(1, min(8, E))), BM=draw(st.sampled_from([16, 32, 64, 128])),
+                routing=draw(st.sampled_from(["softmax", "sigmoid"])), seed=draw(st.integers(0, 10**6)))
+
+
+@settings(max_examples=40, deadline=None, derandomize=True)
+@given(layer_cases())
+def test_random_layers_meet_the_layer_bars(case):
+    from td_benchmark_amd import ops
+
+    print(f"case: random layer {case}", flush=True)
+    T, H, I, E, k, BM = (case[x] for x in ("T", "H", "I", "E", "k", "BM"))
+    c = make_case(T, H, I, E, k, BM, seed=case["seed"], routing=case["routing"])
+    g = to_gpu(c)
+    runner = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, k, BM)
+    y = runner.run(g["x"], g["topk_w"].view(-1), g["topk_ids"].view(-1))
+    torch.cuda.synchronize()
+    y_np = oracle.bf16_to_f32(bf16_bits(y))
+    x32 = oracle.bf16_to_f32(c.x)
+    w1 = dequant_weights_f32(c.w13_q, c.w13_s)
+    w2 = dequant_weights_f32(c.w2_q, c.w2_s)
+    golden = oracle.golden_moe(x32, c.topk_ids, c.topk_w, w1, w2)
+    rep = oracle.compare_outputs(y_np, golden, atol=0.2, rtol=0.0, **oracle.DEFAULT_GATES)
+    assert rep["pass"], rep
+    atol = oracle.calibrated_atol(x32, c.topk_ids, c.topk_w, w1, w2)
+    assert rep["max_abs"] <= atol, (rep, atol)
+    ntpp = int(runner.align.ntpp.item())
+    srt = runner.align.sorted_ids.cpu().numpy()[:ntpp]
+    pos = np.nonzero(srt < c.S)[0]
+    hq, hs = u8_bits(runner.hq), runner.hs.cpu().numpy()
+    hq_slot = np.zeros((c.S, I), np.uint8)
+    hs_slot = np.zeros((c.S, I // 128), np.float32)
+    hq_slot[srt[pos]] = hq[pos]
+    hs_slot[srt[pos]] = hs[pos]
+    ref32 = oracle.dequant_reference(hq_slot, hs_slot, c.topk_ids, c.topk_w, c.w2_q, c.w2_s)
+    rep32 = oracle.compare_outputs(y_np, ref32, atol=0.0, rtol=0.0)
+    assert rep32["max_abs_rel"] <= oracle.MAX_ABS_REL, rep32
