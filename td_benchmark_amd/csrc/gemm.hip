@@ -340,25 +340,53 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
     }
     __syncthreads();
     const int nchunks = g1_store ? 32 : 16;  // 16 B chunks of a row to store
-    for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
-      const int row = ci >> 5, cc = ci & 31;
-      if (cc >= nchunks) continue;
-      const int64_t slot = smSlot[row];
-      if (slot >= g.S) continue;
-      v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + ((cc ^ (row & 15)) << 3));
-      const int64_t n = (cc < 16 ? g0 : g1) * 128 + (cc & 15) * 8;
-      v4i* dst = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
-      if (g.accumulate) {
-        // K-split accumulation: the bf16 partial is added to the bf16 C of the
-        // earlier chunks and rounded again.
-        const v4i old = *dst;
+    if (!g.accumulate) {
+      for (int ci = tid; ci < BM * 32; ci += T::THREADS) {
+        const int row = ci >> 5, cc = ci & 31;
+        if (cc >= nchunks) continue;
+        const int64_t slot = smSlot[row];
+        if (slot >= g.S) continue;
+        const int64_t n = (cc < 16 ? g0 : g1) * 128 + (cc & 15) * 8;
+        *reinterpret_cast<v4i*>(g.C + slot * g.ldc + n) =
+            *reinterpret_cast<const v4i*>(stage_out + row * 256 + ((cc ^ (row & 15)) << 3));
+      }
+    } else {
+      // K-split accumulation: the bf16 partial is added to the bf16 C of the
+      // earlier chunks and rounded again.  A thread's chunks are read in
+      // batches of NBATCH before any of them is written back, so the reads of
+      // C overlap instead of forming one round trip per chunk.
+      constexpr int PER = BM * 32 / T::THREADS;
+      constexpr int NBATCH = PER < 8 ? PER : 8;
+      static_assert(PER * T::THREADS == BM * 32 && PER % NBATCH == 0, "copy-out batches");
+      for (int b0 = 0; b0 < PER; b0 += NBATCH) {
+        v4i old[NBATCH];
+        v4i* dst[NBATCH];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t a = (uint32_t)old[q], b = (uint32_t)val[q];
-          val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(b), hi_bf16(a) + hi_bf16(b));
+        for (int b = 0; b < NBATCH; ++b) {
+          const int ci = tid + (b0 + b) * T::THREADS;
+          const int row = ci >> 5, cc = ci & 31;
+          const int64_t slot = smSlot[row];
+          dst[b] = nullptr;
+          if (cc < nchunks && slot < g.S) {
+            const int64_t n = (cc < 16 ? g0 : g1) * 128 + (cc & 15) * 8;
+            dst[b] = reinterpret_cast<v4i*>(g.C + slot * g.ldc + n);
+            old[b] = *dst[b];
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < NBATCH; ++b) {
+          if (!dst[b]) continue;
+          const int ci = tid + (b0 + b) * T::THREADS;
+          const int row = ci >> 5, cc = ci & 31;
+          v4i val = *reinterpret_cast<const v4i*>(stage_out + row * 256 + ((cc ^ (row & 15)) << 3));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t a = (uint32_t)old[b][q], v = (uint32_t)val[q];
+            val[q] = (int)pack_bf16x2(lo_bf16(a) + lo_bf16(v), hi_bf16(a) + hi_bf16(v));
+          }
+          *dst[b] = val;
         }
       }
-      *dst = val;
     }
   }
 }
