@@ -49,7 +49,9 @@
 // run of the tile's rows per K block.  The weight scales of the tile (both
 // groups, every K block) arrive by direct-to-LDS loads before stage 0.  All
 // direct-to-LDS loads are issued from inline asm (see dma16), weight rows
-// before A rows, at raised wave priority.
+// before A rows, at raised wave priority.  In 16- and 32-row launches, the
+// weight loads of an expert with a single row tile carry the non-temporal
+// hint: that tile is the only reader of its weight tiles.
 //
 // The MFMA takes the weight fragment as its first operand and the activation
 // fragment as its second, so the four results of a lane are four consecutive
@@ -221,6 +223,13 @@ MOE_DEVICE void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "me
 MOE_DEVICE void dma16(const uint8_t* base, uint32_t off, uint8_t* lds) {
   const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+               : "memory");
+}
+// The same load with the non-temporal hint: for weight tiles that one row tile
+// streams alone, so their lines do not displace reused lines in L2.
+MOE_DEVICE void dma16_nt(const uint8_t* base, uint32_t off, uint8_t* lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "s"(m)
                : "memory");
 }
 MOE_DEVICE void dma4(const uint8_t* base, uint32_t off, uint8_t* lds) {
@@ -397,7 +406,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
 // computes its first BM rows; the caller has checked that the rest are padding.
 template <int BM, bool FUSED>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
-                                          int nvalid) {
+                                          int nvalid, bool b_nt) {
   using T = Tile<BM>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* smSB = reinterpret_cast<float*>(smem + T::OFF_SB);  // [2 groups][kMaxKB]
@@ -484,10 +493,24 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
     uint32_t boff = b_off;
     asm volatile("" : "+v"(boff));
     constexpr int HALF = T::NB_W / 2;
+    if constexpr (BM <= 32) {
+      auto issue_b = [&](auto load) {
 #pragma unroll
-    for (int i = 0; i < T::NB_W; ++i) {
-      const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
-      dma16(bbase, boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+        for (int i = 0; i < T::NB_W; ++i) {
+          const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
+          load(bbase, boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+        }
+      };
+      if (b_nt)
+        issue_b(dma16_nt);
+      else
+        issue_b(dma16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < T::NB_W; ++i) {
+        const uint8_t* bbase = (i < HALF ? bg0 : bg1) + (int64_t)(8 * T::NW * (i % HALF)) * g.ldb + kk * 128;
+        dma16(bbase, boff, dst + T::A_BYTES + (wave + T::NW * i) * 1024);
+      }
     }
     const uint8_t* abase = g.A + kk * 128;
 #pragma unroll
@@ -663,7 +686,7 @@ template <int SUB, int BM, bool FUSED>
 __device__ __forceinline__ void short_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
                                            int nvalid) {
   static_assert(Tile<SUB>::THREADS == Tile<BM>::THREADS, "same workgroup size");
-  gemm_tile<SUB, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+  gemm_tile<SUB, FUSED>(g, j, pos0, rows_avail, e, nvalid, false);
   if (FUSED) {
     const int tid = threadIdx.x;
     for (int ci = SUB * 8 + tid; ci < rows_avail * 8; ci += Tile<BM>::THREADS) {
@@ -829,7 +852,11 @@ void grouped_gemm_kernel(GemmArgs g) {
       return;
     }
   }
-  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+  // Weight-streaming tiles (16 and 32 rows) of an expert with one row tile are
+  // the only readers of their weight tiles: those loads carry the
+  // non-temporal hint.  Experts with several row tiles, and taller tiles,
+  // share weight tiles through L2 and load them cached.
+  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, nvalid, BM <= 32 && units == 1);
 }
 
 template <int BM, bool FUSED>
