@@ -882,11 +882,17 @@ class SplitExpertsRunner:
     The activation quant runs once over [T, H]: 1x128 groups never straddle a
     128-aligned chunk, so the codes and scales equal those of quantising each
     K chunk separately (the reference quantises each all-gathered chunk).
+    With ``shared`` the shared expert runs on the layer's own FP8 input and
+    its output is added to the top-k sum, bf16(bf16(sum) + shared), as the
+    reference adds it to each reduced chunk (overlap_forward.py:238-245,
+    315-320); the reduce runs once over all columns (the per-chunk reduce of
+    the reference exists to feed each chunk's reduce-scatter).
     Every buffer is allocated here; ``run`` only launches."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, n_chunks_gateup: int = 4,
-                 n_chunks_down: int = 4, block_size_m: int | None = None):
+                 n_chunks_down: int = 4, block_size_m: int | None = None,
+                 shared: SharedExpertRunner | None = None):
         E, N2, H = _need_weights(w13, w13_scale, "w13")
         _need_weights(w2, w2_scale, "w2")
         if w2.shape != (E, H, N2 // 2):
@@ -898,6 +904,12 @@ class SplitExpertsRunner:
             raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
         self.k_bounds = _split_bounds(H, n_chunks_gateup)
         self.n_bounds = _split_bounds(H, n_chunks_down)
+        if shared is not None and (shared.H != H or shared.max_tokens < num_tokens):
+            raise ValueError("shared expert does not match the layer's hidden size / token count")
+        if shared is not None:
+            shared.prepare(num_tokens)
+        self.shared = shared
+        self.shared_out: torch.Tensor | None = None
         self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
         dev = w13.device
         S1 = max(self.S, 1)
@@ -920,6 +932,8 @@ class SplitExpertsRunner:
             return self.y  # no tokens: [0, H]
         per_token_group_quant_fp8(hidden, out_q=self.q1, out_s=self.s1)
         sorted_ids, eids, ntpp = self.align.run(topk_ids.reshape(-1))
+        if self.shared is not None:
+            self.shared_out = self.shared(self.q1, self.s1)
         for c, (k0, k1) in enumerate(self.k_bounds):
             invoke_moe_kernel_k_split(self.q1, self.w13, self.C13, self.s1, self.w13_scale, None, sorted_ids, eids,
                                       ntpp, False, self.top_k, self.config, K_offset=k0, K_chunk=k1 - k0,
@@ -930,7 +944,7 @@ class SplitExpertsRunner:
         for n0, n1 in self.n_bounds:
             invoke_moe_kernel_n_split(self.hq, self.w2, self.D, self.hs, self.w2_scale, None, w, sorted_ids, eids,
                                       ntpp, True, 1, self.config, N_offset=n0, N_chunk=n1 - n0)
-        moe_sum(self.D[: self.S], self.y, self.top_k)
+        moe_sum(self.D[: self.S], self.y, self.top_k, addend=self.shared_out)
         return self.y
 
 

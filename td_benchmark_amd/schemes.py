@@ -107,6 +107,8 @@ SPEC = SchemeSpec(
         "block_m": TunableSpec(int, 0, "moe_align block size (16/32/64/128/256); 0 picks from rows per expert"),
         "n_chunks": TunableSpec(int, 1, "token chunks pipelined over n_streams HIP streams"),
         "n_streams": TunableSpec(int, 1, "HIP streams for the chunk pipeline (default priority)"),
+        "n_chunks_gateup": TunableSpec(int, 0, "K chunks of W13 (the b schemes' structure); 0 = one pass"),
+        "n_chunks_down": TunableSpec(int, 0, "N chunks of W2 (the b schemes' structure); 0 = one pass"),
     },
 )
 
@@ -126,6 +128,12 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
         raise SchemeConfigError(f"{SPEC.code}.block_m={bm} must be 0 or one of {ops.SUPPORTED_BLOCK_M}")
     if tunables["n_chunks"] < 1 or tunables["n_streams"] < 1:
         raise SchemeConfigError(f"{SPEC.code}: n_chunks and n_streams must be >= 1")
+    kn = (tunables["n_chunks_gateup"], tunables["n_chunks_down"])
+    if min(kn) < 0 or (min(kn) == 0) != (max(kn) == 0):
+        raise SchemeConfigError(f"{SPEC.code}: n_chunks_gateup and n_chunks_down are both 0 or both >= 1")
+    if kn[0] > 0 and tunables["n_chunks"] > 1:
+        raise SchemeConfigError(f"{SPEC.code}: n_chunks_gateup/n_chunks_down (K/N chunks) and n_chunks "
+                                "(token chunks) do not combine")
 
     ckpt = data.ckpt
     w1, w1s = ckpt.w1.fp8.contiguous(), ckpt.w1.scale.float().contiguous()
@@ -143,7 +151,12 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
                     ckpt.shared_w2.fp8.contiguous(), ckpt.shared_w2.scale.float().contiguous())
 
     block_m = bm or None
-    if tunables["n_chunks"] > 1:
+    if kn[0] > 0:
+        # the b schemes' compute stream: K-split W13, N-split W2 (overlap_forward.py:252-321)
+        shared = ops.SharedExpertRunner(*shared_w, max_tokens=T) if shared_w is not None else None
+        runner = ops.SplitExpertsRunner(w1, w1s, w2, w2s, T, k, kn[0], kn[1], block_m, shared=shared)
+        first = runner
+    elif tunables["n_chunks"] > 1:
         runner = ops.ChunkedExpertsRunner(w1, w1s, w2, w2s, T, k, tunables["n_chunks"], tunables["n_streams"],
                                           block_m, shared_weights=shared_w)
         first = runner.runners[0]
@@ -165,7 +178,7 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
 
     def run_staged() -> StageResult:
         runner = live()
-        if isinstance(runner, ops.ChunkedExpertsRunner):
+        if not isinstance(runner, ops.FusedExpertsRunner):
             return StageResult(output=run(), stage_ms={})
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(_STAGES) + 1)]
         ev[0].record()

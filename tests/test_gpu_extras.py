@@ -182,7 +182,8 @@ def _bundle(c, g, shared=None):
     return SimpleNamespace(hidden_local=g["x"], ckpt=ckpt, routing=routing)
 
 
-@pytest.mark.parametrize("tunables", [{}, {"n_chunks": 3, "n_streams": 2}, {"block_m": 64}])
+@pytest.mark.parametrize("tunables", [{}, {"n_chunks": 3, "n_streams": 2}, {"block_m": 64},
+                                      {"n_chunks_gateup": 2, "n_chunks_down": 4}])
 def test_scheme_m1_run_meets_golden_gates(tunables):
     torch = _torch()
     from td_benchmark_amd import schemes
@@ -204,7 +205,7 @@ def test_scheme_m1_run_meets_golden_gates(tunables):
     assert rep["pass"], rep
     staged = inst.run_staged()
     assert np.array_equal(bf16_bits(staged.output), bf16_bits(y))
-    if not tunables.get("n_chunks"):
+    if not tunables.get("n_chunks") and not tunables.get("n_chunks_gateup"):
         assert set(staged.stage_ms) == {"quant", "align", "scales", "w13", "w2", "shared", "reduce"}
     assert inst.diagnostics["scheme"] == "m1" and inst.diagnostics["shared_expert"] is True
     inst.close()
@@ -212,7 +213,7 @@ def test_scheme_m1_run_meets_golden_gates(tunables):
         inst.run()
 
 
-@pytest.mark.parametrize("tunables", [{}, {"n_chunks": 3, "n_streams": 2}])
+@pytest.mark.parametrize("tunables", [{}, {"n_chunks": 3, "n_streams": 2}, {"n_chunks_gateup": 2, "n_chunks_down": 4}])
 def test_scheme_run_allocates_nothing(tunables):
     """The builder allocates every buffer; run() only launches kernels
     (schemes/base.py:45-93; the reference's own lesson on allocation inside the

@@ -117,3 +117,29 @@ def test_split_runner_run_allocates_nothing():
         r.run(g["x"], g["topk_w"], g["topk_ids"])
     torch.cuda.synchronize()
     assert torch.cuda.memory_stats()["allocation.all.allocated"] == before
+
+
+def test_split_runner_adds_the_shared_expert():
+    """With a shared expert the layer output is bf16(bf16(top-k sum) +
+    shared(x)), the shared expert fed the layer's own FP8 input
+    (overlap_forward.py:238-245, 315-320)."""
+    from td_benchmark_amd import ops
+
+    print("case: split runner with shared expert", flush=True)
+    c = make_case(150, 512, 384, 6, 3, 32, seed=9)
+    g = to_gpu(c)
+    rng = np.random.default_rng(19)
+    s1q, s1s = oracle.quant_block128((rng.standard_normal((1, 256, c.H)) * 0.02).astype(np.float32))
+    s2q, s2s = oracle.quant_block128((rng.standard_normal((1, c.H, 128)) * 0.02).astype(np.float32))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    shared = ops.SharedExpertRunner(dev(s1q).view(ops.FP8), dev(s1s), dev(s2q).view(ops.FP8), dev(s2s), c.T)
+    r = ops.SplitExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 2, 3, c.BM, shared=shared)
+    y = bf16_bits(r.run(g["x"], g["topk_w"], g["topk_ids"]))
+    torch.cuda.synchronize()
+    D = bf16_bits(r.D[: c.S])
+    sh = bf16_bits(r.shared_out)
+    sh_alone = bf16_bits(shared(g["x"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(sh, sh_alone)
+    ref = oracle.f32_to_bf16(oracle.bf16_to_f32(oracle.moe_reduce(D, c.T, c.k)) + oracle.bf16_to_f32(sh))
+    assert np.array_equal(y, ref)

@@ -25,12 +25,13 @@ def test_m1_spec_meets_worker_fp8_contract():
     assert spec.weight_dtype == "fp8" and spec.act_quant == "group128"
     assert spec.requires_nvshmem is False
     assert builder is schemes.build
-    assert set(spec.tunables_schema) == {"block_m", "n_chunks", "n_streams"}
+    assert set(spec.tunables_schema) == {"block_m", "n_chunks", "n_streams", "n_chunks_gateup", "n_chunks_down"}
 
 
 def test_validate_tunables_defaults_and_errors():
     spec = schemes.SPEC
-    assert schemes.validate_tunables(spec, {}) == {"block_m": 0, "n_chunks": 1, "n_streams": 1}
+    assert schemes.validate_tunables(spec, {}) == {"block_m": 0, "n_chunks": 1, "n_streams": 1,
+                                                   "n_chunks_gateup": 0, "n_chunks_down": 0}
     assert schemes.validate_tunables(spec, {"n_chunks": 4})["n_chunks"] == 4
     with pytest.raises(schemes.SchemeConfigError, match="violate schema"):
         schemes.validate_tunables(spec, {"bogus": 1})
@@ -50,6 +51,12 @@ def test_build_scheme_rejects_unknown_code_bad_context_and_missing_data():
     with pytest.raises(schemes.SchemeConfigError, match="block_m"):
         schemes.build_scheme(None, SimpleNamespace(world_size=1), object(),
                              SimpleNamespace(code="m1", tunables={"block_m": 48}))
+    # the b schemes' K/N chunk counts (configs/run_v1.yaml: n_chunks_gateup 2, n_chunks_down 4)
+    for bad in ({"n_chunks_gateup": 2}, {"n_chunks_down": 4}, {"n_chunks_gateup": -1, "n_chunks_down": 2},
+                {"n_chunks_gateup": 2, "n_chunks_down": 4, "n_chunks": 2}):
+        with pytest.raises(schemes.SchemeConfigError, match="n_chunks"):
+            schemes.build_scheme(None, SimpleNamespace(world_size=1), object(),
+                                 SimpleNamespace(code="m1", tunables=bad))
 
 
 @pytest.mark.parametrize("name", SCRIPTS)
