@@ -39,11 +39,12 @@
 // uniform base plus a fixed 32-bit lane offset).  For TM = 64 and 128 a 3-stage
 // ring (A TM*128 B + B 32 KiB per stage, plus the A scales): step k waits until
 // only step k+1's loads are in flight, passes one barrier, issues step k+2's
-// loads into the buffer freed at step k-1, then computes.  TM = 16 and 32 (the
-// weight-streaming decode tiles) keep a 4-stage ring, two younger stages in
+// loads into the buffer freed at step k-1, then computes.  TM = 16 (a
+// weight-streaming decode tile) keeps a 4-stage ring, two younger stages in
 // flight.  At TM = 256 three 64 KiB stages exceed the LDS, so the ring has two
 // stages and every step waits for all of its loads; A rows of subtiles without
-// a valid row are then not fetched.  The activation scales of a stage are one
+// a valid row are then not fetched.  TM = 32 (the default decode tile) also
+// has two stages, in two workgroups per CU that stream independently.  The activation scales of a stage are one
 // 4-byte direct-to-LDS load per row: from the row's own scale row, or -- when
 // they are laid out K-major by sorted position (as_pos_ld) -- one contiguous
 // run of the tile's rows per K block.  The weight scales of the tile (both
@@ -97,8 +98,11 @@ struct Tile {
   // waves along M: 4 x 2 waves of 64 x 128 at BM = 256 (fewer LDS bytes per MFMA)
   static constexpr int WM = BM == 256 ? 4 : ((NW == 8 || BM == 128) ? 2 : 1);
   // LDS ring depth: three 64 KiB stages of the 256-row tile exceed 160 KiB;
-  // the 34-36 KiB stages of the 16- and 32-row tiles (weight streaming) fit four
-  static constexpr int KS = BM == 256 ? 2 : (BM <= 32 ? 4 : 3);
+  // the 34 KiB stages of the 16-row tile (weight streaming) fit four; the
+  // 32-row tile runs two workgroups per CU with two 36 KiB stages each, so one
+  // workgroup's pipeline fill and epilogue overlap the other's weight stream
+  static constexpr int KS = (BM == 256 || BM == 32) ? 2 : (BM == 16 ? 4 : 3);
+  static constexpr int WG_PER_CU = BM == 32 ? 2 : 1;
   static constexpr int WN = NW / WM;              // waves along N
   static constexpr int RS = BM / WM / 16;         // 16-row subtiles per wave
   static constexpr int CS = 8 / WN;               // 16-col subtiles per wave per group
@@ -126,7 +130,7 @@ struct Tile {
   static constexpr int OFF_ROW = OFF_RED + WN * BM * 4;  // per-row slot id and routed weight
   static constexpr int LDS_BYTES = OFF_ROW + BM * 8;
   static_assert(BM * 512 <= OFF_SA, "bf16 output staging must fit in the operand ring");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(LDS_BYTES * WG_PER_CU <= 160 * 1024, "LDS budget");
   static_assert(VM * (KS - 2) < 64, "vmcnt immediate");
 };
 
@@ -705,7 +709,7 @@ constexpr int kernel_lds() {
 
 template <int BM, bool FUSED>
 __global__ __launch_bounds__(Tile<BM>::THREADS)
-__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4, Tile<BM>::NW / 4)))
+__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU, Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU)))
 void grouped_gemm_kernel(GemmArgs g) {
   using T = Tile<BM>;
   static_assert(BM <= kTailRows || Tile<kTailRows>::LDS_BYTES <= kernel_lds<BM>(),
