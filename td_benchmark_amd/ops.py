@@ -527,18 +527,32 @@ def gemm_tile_rows(block_size_m: int, num_slots: int, num_experts: int, tile_m: 
 
 def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, int]:
     """Replacement for vLLM's try_get_optimal_moe_config (overlap_forward.py:
-    153-163): picks BLOCK_SIZE_M from the average rows per expert so that the
-    padding of small experts stays small.  Below 48 rows per expert (decode)
-    it is 32, not 16: those layers stream their weights, and the 32-row tile
-    (8 waves, a 4-stage LDS ring) streams them faster than the 16-row one
-    (4 waves) -- 1365 vs 1389 us for the DeepSeek-V3 decode layer on MI355X."""
+    153-163): picks BLOCK_SIZE_M from the average rows per expert, avg =
+    num_tokens * top_k / num_experts, by a sweep of the whole layer over
+    block sizes 16-256 on MI355X (four expert shapes: H/I/E/top-k of
+    DeepSeek-V3, Mixtral, Qwen3-30B-A3B and the reference's v1 GroupGEMM
+    sweep, 4-1024 rows per expert):
+
+    * avg <= 40: 32.  The layer streams its weights; the 32-row tile streams
+      them faster than the 16-row one and wastes less than taller blocks.
+    * avg <= 100: 128.  Most experts fit one block; a 128-row tile reads
+      fewer LDS bytes per MFMA than a 64-row one (v1 shape, 64 rows per
+      expert: 195 us against 209 at 64; DeepSeek-V3: 2208 against 2606).
+    * above: 256, so that an expert's rows stay in one tile instead of
+      spilling a few rows into a second one (128 rows per expert: 237 against
+      244 us at 128; Qwen3 at 160: 241 against 299) -- except when the average
+      sits at 240-288 rows, where half the experts would spill a few rows into
+      a second 256-row block and 128-row blocks split them evenly over two
+      256-row tiles instead (DeepSeek-V3 at 256: 3920 against 4058 us)."""
     avg = num_tokens * top_k / max(num_experts, 1)
-    if avg <= 48:
+    if avg <= 40:
         bm = 32
-    elif avg <= 160:
-        bm = 64
-    else:
+    elif avg <= 100:
         bm = 128
+    elif 240 <= avg <= 288:
+        bm = 128
+    else:
+        bm = 256
     return {"BLOCK_SIZE_M": bm, "BLOCK_SIZE_N": 256, "BLOCK_SIZE_K": 128}
 
 

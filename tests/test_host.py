@@ -23,7 +23,10 @@ def test_moe_config_block_m_tracks_rows_per_expert():
     # decode: 128*8/256 = 4 rows per expert -> 32 (its weight stream is faster than 16's)
     assert ops.get_moe_config(128, 256, 8)["BLOCK_SIZE_M"] == 32
     assert ops.get_moe_config(64, 4, 2)["BLOCK_SIZE_M"] == 32   # 32 rows per expert
-    assert ops.get_moe_config(512, 64, 8)["BLOCK_SIZE_M"] == 64
+    assert ops.get_moe_config(512, 64, 8)["BLOCK_SIZE_M"] == 128  # 64 rows per expert
+    assert ops.get_moe_config(1024, 64, 8)["BLOCK_SIZE_M"] == 256  # 128: one tile per expert
+    assert ops.get_moe_config(2560, 64, 8)["BLOCK_SIZE_M"] == 256  # 320
+    assert ops.get_moe_config(16384, 128, 8)["BLOCK_SIZE_M"] == 256  # Qwen3 one pass: 1024
     for T in (1, 7, 100, 4096, 65536):
         cfg = ops.get_moe_config(T, 128, 8)
         assert cfg["BLOCK_SIZE_M"] in ops.SUPPORTED_BLOCK_M
