@@ -32,7 +32,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=["dsv3", "mixtral"])
+@pytest.fixture(scope="module", params=["dsv3", "mixtral", "qwen3"])
 def layer(request):
     from td_benchmark_amd import ops, workloads
     wl = workloads.CONFIGS[request.param]
