@@ -87,6 +87,11 @@ namespace moe {
 constexpr int kXcds = 8;
 constexpr int kMaxKB = 128;  // K <= 16384
 constexpr int kTailRows = 64;  // row tiles with at most this many valid rows run the short body
+// Plain launches with K of at least this many columns order the tiles of an
+// n-tile group column-major (Mixtral's W2, K = 14336: 1-3 % faster; W13 of
+// every shape and the W2 of DeepSeek-V3 and Qwen3, K <= 7168, lose 1-7 % that
+// way).
+constexpr int64_t kColMajorK = 8192;
 // MFMAs issued between an MFMA and the FMAs that scale its result: the VALU
 // reads a result that is complete, without hazard waits.
 constexpr int kScaleLag = 2;
@@ -796,12 +801,16 @@ void grouped_gemm_kernel(GemmArgs g) {
   // Inside a run, n-tiles go in groups of GG, row-tile-major within a group:
   // the GG workgroups that share an A tile start together and reuse it from
   // L2, and a weight tile is still read by all row tiles of the run close in time.
+  // Plain launches with a long K (kColMajorK and up: W2 of wide experts, whose
+  // weight tiles are large) go column-major within a group instead: the row
+  // tiles that share a weight tile start together.
   constexpr int64_t GG = 4;  // 2, 8 and 16 (W13), 2, 3, 7 and 14 (W2) measured slower
   const int64_t gj0 = in_run / (GG * units) * GG;
   const int64_t gsz = (g.n_tiles - gj0) < GG ? (g.n_tiles - gj0) : GG;
   const int64_t in_grp = in_run - gj0 * units;
-  const int64_t j = gj0 + in_grp % gsz;
-  const int64_t u = in_grp / gsz;               // row tile of the run
+  const bool by_col = !FUSED && g.K >= kColMajorK;
+  const int64_t j = gj0 + (by_col ? in_grp / units : in_grp % gsz);
+  const int64_t u = by_col ? in_grp % units : in_grp / gsz;  // row tile of the run
   const int64_t base = run / units, n_short = units - run % units;  // n_short tiles of `base` blocks
   const int64_t b = b0 + (u < n_short ? u * base : n_short * base + (u - n_short) * (base + 1));
   const int64_t pos0 = b * g.bma;               // sorted position of tile row 0

@@ -26,7 +26,7 @@ import pytest
 
 import oracle
 from moe_cases import a7_account, a7_assert, bf16_bits, u8_bits
-from tile_map import pick_tiles, tile_map, tile_positions
+from tile_map import COL_MAJOR_K, pick_tiles, tile_map, tile_positions
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -118,7 +118,7 @@ def test_w2_whole_tiles(layer):
     wl, d, runner, C13, h, host, tile_m = layer
     S, H, BM = wl.S, wl.H, wl.block_m
     n_tiles = (H // 128 + 1) // 2
-    tiles = tile_map(host["eids"], host["ntpp"], BM, tile_m, n_tiles)
+    tiles = tile_map(host["eids"], host["ntpp"], BM, tile_m, n_tiles, col_major=wl.I >= COL_MAJOR_K)
     picked = pick_tiles(tiles, host["sorted"], S)
     D = bf16_bits(runner.D[:S])
     for name, ti in picked.items():

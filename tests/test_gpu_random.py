@@ -148,3 +148,46 @@ def test_random_layers_meet_the_layer_bars(case):
     ref32 = oracle.dequant_reference(hq_slot, hs_slot, c.topk_ids, c.topk_w, c.w2_q, c.w2_s)
     rep32 = oracle.compare_outputs(y_np, ref32, atol=0.0, rtol=0.0)
     assert rep32["max_abs_rel"] <= oracle.MAX_ABS_REL, rep32
+
+
+@pytest.mark.parametrize("which", ["w13_plain", "w2_routed"])
+def test_long_k_plain_gemms_within_the_bound(which):
+    """Plain launches with K >= 8192 order each n-tile group column-major (the
+    row tiles that share a weight tile start together); two row tiles per
+    expert (512 rows at 256-row tiles), so the order matters, against the
+    oracle within the GEMM bound (overlap/kernels.py:95-214)."""
+    from td_benchmark_amd import ops
+
+    print(f"case: long-K plain GEMM {which}", flush=True)
+    rng = np.random.default_rng(21)
+    T, E, k, BM, K = 512, 2, 2, 64, 8192
+    S = T * k
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k), dtype=np.float32) + np.float32(0.05)
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    srt, eids, ntpp = oracle.moe_align(ids, E, BM)
+    d_srt, d_eids = _gpu(srt), _gpu(eids)
+    d_ntpp = torch.tensor([ntpp], dtype=torch.int32, device="cuda")
+    assert ops.gemm_tile_rows(BM, S, E) == 256
+    N = 256
+    B = _fp8_codes(rng, (E, N, K))
+    Bs = (rng.random((E, N // 128, K // 128), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    if which == "w13_plain":
+        x = oracle.f32_to_bf16(rng.standard_normal((T, K), dtype=np.float32))
+        A, As = oracle.quant_group128(x)
+        ref, mag = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, k, with_magnitude=True)
+        C = torch.zeros((T, k, N), dtype=torch.bfloat16, device="cuda")
+        ops.dispatch_fused_moe_kernel(_gpu(A, torch.float8_e4m3fn), _gpu(B, torch.float8_e4m3fn), C, _gpu(As),
+                                      _gpu(Bs), None, None, d_srt, d_eids, d_ntpp, False, k, {"BLOCK_SIZE_M": BM})
+    else:
+        A = _fp8_codes(rng, (srt.size, K))
+        As = (rng.random((srt.size, K // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
+        ref, mag = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
+                                       topk_w=w.ravel(), with_magnitude=True)
+        C = torch.zeros((S, 1, N), dtype=torch.bfloat16, device="cuda")
+        ops.dispatch_fused_moe_kernel(_gpu(A, torch.float8_e4m3fn), _gpu(B, torch.float8_e4m3fn), C, _gpu(As),
+                                      _gpu(Bs), None, _gpu(w.ravel()), d_srt, d_eids, d_ntpp, True, 1,
+                                      {"BLOCK_SIZE_M": BM}, a_by_pos=True)
+    torch.cuda.synchronize()
+    bad = oracle.gemm_close(bf16_bits(C).reshape(S, N), ref, mag)
+    assert not bad.any(), f"{which}: {int(bad.sum())} of {bad.size} outside the bound"

@@ -113,15 +113,16 @@ def test_tile_map_covers_every_position_once(T, E, k, BM, tile_m, n_tiles, routi
     rng = np.random.default_rng(T + E)
     ids, _ = route(rng.standard_normal((T, E), dtype=np.float32), k, routing, rng)
     srt, eids, ntpp = oracle.moe_align(ids, E, BM)
-    tiles = tile_map(eids, ntpp, BM, tile_m, n_tiles)
-    cov = np.zeros((ntpp, n_tiles), np.int32)
-    for ti in tiles:
-        assert ti.rows % BM == 0 and 0 < ti.rows <= max(tile_m, BM)
-        assert len(set(eids[ti.pos0 // BM:(ti.pos0 + ti.rows) // BM].tolist())) == 1
-        cov[ti.pos0:ti.pos0 + ti.rows, ti.j] += 1
-    assert cov.min() == 1 and cov.max() == 1
-    ts = sorted(t.t for t in tiles)
-    assert len(set(ts)) == len(ts) and max(t.xcd for t in tiles) < XCDS
+    for col_major in (False, True):  # the group orders of short-K and long-K plain launches
+        tiles = tile_map(eids, ntpp, BM, tile_m, n_tiles, col_major=col_major)
+        cov = np.zeros((ntpp, n_tiles), np.int32)
+        for ti in tiles:
+            assert ti.rows % BM == 0 and 0 < ti.rows <= max(tile_m, BM)
+            assert len(set(eids[ti.pos0 // BM:(ti.pos0 + ti.rows) // BM].tolist())) == 1
+            cov[ti.pos0:ti.pos0 + ti.rows, ti.j] += 1
+        assert cov.min() == 1 and cov.max() == 1
+        ts = sorted(t.t for t in tiles)
+        assert len(set(ts)) == len(ts) and max(t.xcd for t in tiles) < XCDS
     picked = pick_tiles(tiles, srt, T * k)
     assert {f"xcd{x}_first" for x in {t.xcd for t in tiles}} <= set(picked)
 

@@ -49,8 +49,13 @@ def runs_of(eids: np.ndarray) -> list[tuple[int, int]]:
     return out
 
 
-def tile_map(eids: np.ndarray, ntpp: int, bma: int, tile_m: int, n_tiles: int) -> list[TileInfo]:
-    """Every active tile of one launch (idle tile ids are left out)."""
+COL_MAJOR_K = 8192  # plain launches with K >= this order a group column-major
+
+
+def tile_map(eids: np.ndarray, ntpp: int, bma: int, tile_m: int, n_tiles: int,
+             col_major: bool = False) -> list[TileInfo]:
+    """Every active tile of one launch (idle tile ids are left out).
+    ``col_major``: the group order of plain launches with K >= COL_MAJOR_K."""
     n_blocks = ntpp // bma
     eids = np.asarray(eids[:n_blocks])
     total = n_blocks * n_tiles
@@ -64,8 +69,8 @@ def tile_map(eids: np.ndarray, ntpp: int, bma: int, tile_m: int, n_tiles: int) -
             gj0 = in_run // (GROUP * units) * GROUP
             gsz = min(n_tiles - gj0, GROUP)
             in_grp = in_run - gj0 * units
-            j = gj0 + in_grp % gsz
-            u = in_grp // gsz
+            j = gj0 + (in_grp // units if col_major else in_grp % gsz)
+            u = in_grp % units if col_major else in_grp // gsz
             b = b0 + (u * base if u < n_short else n_short * base + (u - n_short) * (base + 1))
             rows = (base if u < n_short else base + 1) * bma
             t = b0 * n_tiles + in_run
