@@ -23,7 +23,7 @@
 // split evenly over the expert's tiles, so a weight tile is fetched once per
 // up to 256 rows.  8 waves (2 per SIMD, so one wave's MFMAs run while the other
 // waits on LDS or the barrier) for TM >= 32, 4 for TM = 16; at TM = 256 they
-// are 4 x 2 waves of 64 x 128.  The K step is 128 = one scale block, and every
+// are 4 x 2 waves of 64 x 128.  TM = 32 runs two workgroups per CU.  The K step is 128 = one scale block, and every
 // K step is exactly one 16x16x128 MFMA per 16x16 output subtile started from
 // zero, so the per-block scales are applied as acc = fma(partial,
 // a_s[row]*b_s[group], acc) (kScaleLag MFMAs later) with no second
