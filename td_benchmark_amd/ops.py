@@ -27,9 +27,20 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# The current stream's raw handle straight from torch's C++ side (the accessor
+# torch's own code generator uses); torch.cuda.current_stream() builds a Stream
+# object through a device-index lookup and costs about 2.7 us a call, which a
+# launch-bound layer of seven kernels pays on every op.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_CUR_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+
+
 def _stream(stream: torch.cuda.Stream | None = None) -> ctypes.c_void_p:
-    s = torch.cuda.current_stream() if stream is None else stream
-    return ctypes.c_void_p(s.cuda_stream)
+    if stream is None:
+        if _RAW_STREAM is not None and _CUR_DEVICE is not None:
+            return ctypes.c_void_p(_RAW_STREAM(_CUR_DEVICE()))
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
 
 
 def _need(t: torch.Tensor, name: str, dtype: torch.dtype | None = None,

@@ -106,3 +106,19 @@ def test_runners_check_weights_and_inputs(case):
     with pytest.raises(ValueError, match="input_scale must have shape"):
         sh(q, s[:, :1].contiguous())
     torch.cuda.synchronize()
+
+
+def test_launch_stream_is_torchs_current_stream():
+    """Every launch goes to torch's current stream: the raw handle the ops read
+    equals torch.cuda.current_stream(), also inside a stream context."""
+    from td_benchmark_amd import ops
+
+    print("case: launch stream", flush=True)
+    def raw():  # the null (default) stream's handle is 0; ctypes reads it back as None
+        return ops._stream().value or 0
+
+    assert raw() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert raw() == side.cuda_stream == torch.cuda.current_stream().cuda_stream != 0
+    assert raw() == torch.cuda.current_stream().cuda_stream
