@@ -244,21 +244,31 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # The layer as a caller runs it: K steps, one event pair around each for the
+    # per-step samples and nothing between its launches.
+    sev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        step(events[i])
+        sev[i][0].record()
+        step()
+        sev[i][1].record()
     end.record()
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / args.steps
     ms_single = ms_per_step
+    single_stats = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in sev])
+    # Per-stage times from K more steps with an event between every two
+    # launches (on launch-bound layers those records add host time, which is
+    # why the layer time above is taken without them).
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
     stage_ms = {name: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
                 for j, name in enumerate(STAGES)}
-    # per-step samples: each step's first to last event (the gaps between
-    # steps, a few microseconds of launch, fall outside them)
-    single_stats = summarize_samples([ev[0].elapsed_time(ev[-1]) * 1e3 for ev in events])
     stage_stats = {name: summarize_samples([ev[j].elapsed_time(ev[j + 1]) * 1e3 for ev in events])
                    for j, name in enumerate(STAGES) if name in ("w13", "w2")}
     step_stats = single_stats
