@@ -23,7 +23,7 @@ from hypothesis import given, settings
 from hypothesis import strategies as st
 
 import oracle
-from moe_cases import bf16_bits, dequant_weights_f32, make_case, to_gpu, u8_bits
+from moe_cases import a7_account, a7_assert, bf16_bits, dequant_weights_f32, make_case, to_gpu, u8_bits
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -191,3 +191,50 @@ def test_long_k_plain_gemms_within_the_bound(which):
     torch.cuda.synchronize()
     bad = oracle.gemm_close(bf16_bits(C).reshape(S, N), ref, mag)
     assert not bad.any(), f"{which}: {int(bad.sum())} of {bad.size} outside the bound"
+
+
+@st.composite
+def fused_cases(draw):
+    E = draw(st.integers(1, 24))
+    BM = draw(st.sampled_from([16, 32, 64, 128]))
+    return dict(T=draw(st.integers(1, 160)), H=128 * draw(st.integers(1, 4)), I=128 * draw(st.integers(1, 3)),
+                E=E, k=draw(st.integers(1, min(8, E))), BM=BM,
+                tile_m=draw(st.sampled_from([0] + [t for t in (16, 32, 64, 128, 256) if t >= BM])),
+                routing=draw(st.sampled_from(["softmax", "sigmoid"])), seed=draw(st.integers(0, 10**6)))
+
+
+@settings(max_examples=30, deadline=None, derandomize=True)
+@given(fused_cases())
+def test_random_fused_w13_equals_the_unfused_chain(case):
+    """The fused W13 epilogue (SiLU*up and the 1x128 quant of h, written by
+    sorted position; overlap_forward.py:261-284) equals the GPU's own unfused
+    chain -- plain GEMM, silu_and_mul, quant -- bit for bit at every drawn
+    shape and tile height, and its codes meet the intermediate-code account
+    against the CPU chain (tests/moe_cases.py, a7_assert)."""
+    from td_benchmark_amd import ops
+
+    print(f"case: random fused W13 {case}", flush=True)
+    T, H, I, E, k, BM, tm = (case[x] for x in ("T", "H", "I", "E", "k", "BM", "tile_m"))
+    c = make_case(T, H, I, E, k, BM, seed=case["seed"], routing=case["routing"])
+    g = to_gpu(c)
+    q1, s1 = ops.per_token_group_quant_fp8(g["x"])
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(g["topk_ids"], BM, E)
+    hq, hs = ops.gemm_w13_silu_quant(q1, s1, g["w13"], g["w13_s"], sorted_ids, eids, ntpp, c.S, k, BM, tile_m=tm)
+    C = torch.empty((c.S, 2 * I), dtype=torch.bfloat16, device="cuda")
+    ops.dispatch_fused_moe_kernel(q1, g["w13"], C, s1, g["w13_s"], None, None, sorted_ids, eids, ntpp,
+                                  False, k, {"BLOCK_SIZE_M": BM}, tile_m=tm)
+    h = torch.empty((c.S, I), dtype=torch.bfloat16, device="cuda")
+    ops.silu_and_mul(h, C)
+    q2, s2 = ops.per_token_group_quant_fp8(h)
+    torch.cuda.synchronize()
+    n = int(ntpp.item())
+    srt = sorted_ids.cpu().numpy()[:n]
+    pos = np.nonzero(srt < c.S)[0]
+    slots = srt[pos]
+    hq_np, hs_np = u8_bits(hq)[pos], hs.cpu().numpy()[pos]
+    assert np.array_equal(hq_np, u8_bits(q2)[slots])
+    assert np.array_equal(hs_np.view(np.uint32), s2.cpu().numpy()[slots].view(np.uint32))
+    st_ = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, BM)
+    rep = a7_account(hq_np, hs_np, bf16_bits(h)[slots], bf16_bits(C)[slots], st_["q2"][slots], st_["s2"][slots],
+                     st_["h"][slots], st_["c13"][slots], st_["c13_f32"][slots], st_["mag13"][slots])
+    a7_assert(rep, f"random fused W13 {case}")
