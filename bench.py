@@ -14,7 +14,9 @@ region.  ``roofline`` describes the dominant kernel (the W13 GEMM).
 ``layer_us_stats`` gives avg/min/med/p95/std over the per-step samples
 (moe_bench/timing.py:23-34).  ``cpu_baseline`` times the reference's torch CPU
 golden path (restated in oracle/golden_torch.py, all host cores) on a bounded
-sample of the same workload.
+sample of the same workload.  ``shared_expert`` times the shared expert (one
+E=1, top-1 expert of the same hidden and intermediate size) on the layer's own
+FP8 input, outside the layer time.
 """
 from __future__ import annotations
 
@@ -101,6 +103,51 @@ def cpu_model_name() -> str:
     except OSError:
         pass
     return ""
+
+
+def shared_expert_leg(runner, wl, steps: int, warmup: int) -> dict:
+    """The shared expert beside the routed layer: one expert (E = 1, top-1)
+    of the layer's hidden size with intermediate size I (the reference's
+    shared_intermediate default, config.py ShapeCfg), weights N(0, H^-0.5) and
+    N(0, I^-0.5) block-quantised 128x128 (data/checkpoint.py:64-66), run on
+    the layer's own FP8 input with its build-time align
+    (schemes/shared_expert.py:81-148).  Each call is the fused W13 (SiLU*up +
+    1x128 quant) and the W2 GEMM; the two are timed together with HIP events
+    around every call."""
+    import torch
+
+    from td_benchmark_amd import ops, workloads
+
+    T, H, I = wl.T, wl.H, wl.I
+    gen = torch.Generator(device="cuda").manual_seed(wl.seed + 1)
+    w1 = torch.randn((1, 2 * I, H), generator=gen, device="cuda") * H ** -0.5
+    w2 = torch.randn((1, H, I), generator=gen, device="cuda") * I ** -0.5
+    w1q, w1s = ops.quantize_block128(w1)
+    w2q, w2s = ops.quantize_block128(w2)
+    del w1, w2
+    sh = ops.SharedExpertRunner(w1q, w1s, w2q, w2s, max_tokens=T)
+    for _ in range(warmup):
+        sh(runner.q1, runner.s1)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        a.record()
+        sh(runner.q1, runner.s1)
+        b.record()
+    torch.cuda.synchronize()
+    stats = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in ev])
+    one = workloads.Workload("shared", T, H, I, 1, 1, sh.BM, "softmax")
+    ntpp = int(sh._align_for(T).ntpp.item())
+    by = stage_bytes(one, ntpp, 1, sh.BM)
+    flop = 6.0 * T * H * I
+    sec = stats["avg"] / 1e6
+    bytes_ = by["w13"] + by["w2"]
+    return {"us": stats["avg"], "us_stats": stats, "T": T, "H": H, "I": I, "block_size_m": sh.BM,
+            "gemm_tile_m": ops.gemm_tile_rows(sh.BM, T, 1), "flop": flop, "bytes": bytes_,
+            "TFLOP/s": flop / sec / 1e12, "mfma_frac": flop / sec / 1e12 / PEAK_FP8_TFLOPS,
+            "GB/s": bytes_ / sec / 1e9, "hbm_frac": bytes_ / sec / 1e9 / PEAK_HBM_GBS,
+            "bound": "mfma" if flop / (PEAK_FP8_TFLOPS * 1e12) >= bytes_ / (PEAK_HBM_GBS * 1e9) else "hbm",
+            "input": "the routed layer's FP8 activations and 1x128 scales (no second quant)"}
 
 
 def _time_cpu(fn, warmup: int, repeat: int) -> dict:
@@ -200,6 +247,8 @@ def main() -> int:
     ap.add_argument("--block-m", type=int, default=0, help="override the workload's block_size_m")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline compute")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-shared", action="store_true",
+                    help="skip the shared-expert leg (one E=1, top-1 expert on the layer's FP8 input)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the multi-GPU expert/tensor-parallel "
@@ -387,6 +436,8 @@ def main() -> int:
         "active_experts": active,
         "roofline": roof,
     }
+    if not args.no_shared:
+        result["shared_expert"] = shared_expert_leg(runner, wl, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(data, wl, args.cpu_budget)
         n_rows = min(wl.T, 1024) * wl.top_k

@@ -264,11 +264,6 @@ int moe_reduce_topk_add(const void* D_bf16, const void* addend_bf16, int64_t T, 
 int moe_fp8_dequant_sum(const void* q_fp8, const float* scales, int64_t R, int64_t M, int64_t N,
                         int64_t scale_ld, void* out_bf16, int64_t out_ld, void* stream);
 
-/* Test hook (no reference counterpart): one 16x16x128 FP8 MFMA through the
- * GEMM's own LDS swizzle, fragment loader and output mapping.
- * A [16,128], B [16,128] e4m3fn -> C [16,16] fp32 = A . B^T. */
-int moe_debug_mfma_probe(const void* A, const void* B, float* C, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

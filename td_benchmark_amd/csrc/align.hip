@@ -320,16 +320,25 @@ extern "C" int64_t moe_align_workspace_bytes(int64_t S, int32_t E) {
   return 4 * (n_chunks * E + S + 2 * (int64_t)E + 1) + 256;
 }
 
-static int align_impl(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM, const int32_t* expert_map,
-                      int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
-                      void* workspace, void* stream) {
+// Every argument check of an align call, before any device work; the
+// workspace pointer is checked only when the caller supplies one.
+static int align_args(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM, int32_t* sorted_ids,
+                      int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, bool need_ws, const void* workspace) {
   if (S < 0) return kErrBadShape;
   if (E <= 0 || E > kAlignMaxExperts) return kErrBadExperts;
   if (!block_m_ok(BM)) return kErrBadBlockSize;
-  if (!sorted_ids || !expert_ids || !ntpp || !workspace || (S > 0 && !topk_ids))
+  if (!sorted_ids || !expert_ids || !ntpp || (need_ws && !workspace) || (S > 0 && !topk_ids))
     return kErrNullPointer;
   if (max_padded < moe_align_max_padded(S, E, BM)) return kErrCapacity;
   if (S > 0x7FFFFFFF - 1 || max_padded > 0x7FFFFFFF) return kErrBadShape;
+  return kOk;
+}
+
+static int align_impl(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM, const int32_t* expert_map,
+                      int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
+                      void* workspace, void* stream) {
+  const int arg_rc = align_args(topk_ids, S, E, BM, sorted_ids, expert_ids, ntpp, max_padded, true, workspace);
+  if (arg_rc != kOk) return arg_rc;
   hipStream_t st = (hipStream_t)stream;
   int nbits0 = 0;
   while ((1 << nbits0) < E) ++nbits0;
@@ -423,9 +432,10 @@ static int scratch_for_current_device(void** out) {
 extern "C" int moe_align_block_size_noalloc(const int32_t* topk_ids, int64_t S, int32_t E, int32_t BM,
                                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp,
                                             int64_t max_padded, void* stream) {
-  const int64_t need = moe_align_workspace_bytes(S, E);
-  if (need < 0) return S < 0 ? kErrBadShape : kErrBadExperts;
-  if (need > kNoAllocScratchBytes) return kErrCapacity;
+  // every argument is checked before the device is touched (symbol lookup)
+  const int arg_rc = align_args(topk_ids, S, E, BM, sorted_ids, expert_ids, ntpp, max_padded, false, nullptr);
+  if (arg_rc != kOk) return arg_rc;
+  if (moe_align_workspace_bytes(S, E) > kNoAllocScratchBytes) return kErrCapacity;
   void* ws = nullptr;
   const int rc = scratch_for_current_device(&ws);
   if (rc != kOk) return rc;

@@ -79,6 +79,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "mfma_frag.hpp"
 
 #define MOE_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -196,24 +197,6 @@ static inline void dense_strides(GemmArgs& g) {
   g.accumulate = 0;
 }
 
-// Chunk swizzle of an LDS row (see the header comment).
-MOE_HOST_DEVICE int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-// LDS slot of logical 16 B chunk c in row `row`, and its inverse (an involution).
-MOE_HOST_DEVICE int slot_of(int c, int row) { return (c ^ swz(row)) & 7; }
-
-MOE_DEVICE v4f mfma_fp8(v8i a, v8i b) {
-  const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
-}
-
-// A 32-byte fragment from two per-lane LDS bases plus a compile-time offset.
-template <int OFF>
-MOE_DEVICE v8i frag_at(const uint8_t* base0, const uint8_t* base1) {
-  const v4i x = *reinterpret_cast<const v4i*>(base0 + OFF);
-  const v4i y = *reinterpret_cast<const v4i*>(base1 + OFF);
-  return (v8i){x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-}
-
 // Barrier / counter waits as compiler-opaque memory clobbers, so that no LDS
 // access is moved across them and no fence forces a full vmcnt(0) drain.
 MOE_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
@@ -227,25 +210,30 @@ MOE_DEVICE void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "me
 // reads of a K step could not overlap each other.  The kernel waits for these
 // loads itself (s_waitcnt vmcnt + s_barrier before the stage is read).  M0
 // holds the LDS destination (a wave-uniform byte address), the global address
-// is the uniform 64-bit base plus the lane's 32-bit offset.  M0 is written
-// here only: the kernels that call these use no other M0-based instruction.
+// is the uniform 64-bit base plus the lane's 32-bit offset.  M0 is declared
+// clobbered (the compiler reserves it and warns that it may not honour the
+// clobber), and it is written here only: the kernels that call these use no
+// other M0-based instruction, which a test checks on the compiled assembly.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 MOE_DEVICE void dma16(const uint8_t* base, uint32_t off, uint8_t* lds) {
   const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
-               : "memory");
+               : "memory", "m0");
 }
 // The same load with the non-temporal hint: for weight tiles that one row tile
 // streams alone, so their lines do not displace reused lines in L2.
 MOE_DEVICE void dma16_nt(const uint8_t* base, uint32_t off, uint8_t* lds) {
   const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "s"(m)
-               : "memory");
+               : "memory", "m0");
 }
 MOE_DEVICE void dma4(const uint8_t* base, uint32_t off, uint8_t* lds) {
   const uint32_t m = (uint32_t)(uintptr_t)MOE_LDS(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m)
-               : "memory");
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Column scale groups of n-tile j: W13 gate group j and up group I/128 + j; the
 // plain GEMM groups 2j and 2j+1 (the second absent past N).
@@ -1244,31 +1232,4 @@ extern "C" int moe_gemm_w13_silu_quant(const void* Aq, const float* A_scale, con
                                        void* stream) {
   return moe_gemm_w13_silu_quant_tiled(Aq, A_scale, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k,
                                        H, I, E, BM, max_padded, 0, hq, hs, stream);
-}
-
-// Layout probe: one wave computes C[16][16] = A[16][128] . B[16][128]^T through
-// the GEMM's LDS row swizzle, fragment loader, MFMA call and output mapping.
-__global__ void mfma_probe_kernel(const uint8_t* A, const uint8_t* B, float* C) {
-  __shared__ __attribute__((aligned(16))) uint8_t sAB[2 * 16 * 128];
-  const int lane = threadIdx.x;
-  for (int ci = lane; ci < 256; ci += 64) {
-    const int row = (ci >> 3) & 15, cc = ci & 7;
-    const uint8_t* src = (ci < 128 ? A : B) + row * 128 + cc * 16;
-    *reinterpret_cast<v4i*>(sAB + (ci < 128 ? 0 : 2048) + row * 128 + (slot_of(cc, row) << 4)) =
-        *reinterpret_cast<const v4i*>(src);
-  }
-  __syncthreads();
-  const int fr = lane & 15, kseg = lane >> 4;
-  const uint8_t* p0 = sAB + fr * 128 + (slot_of(2 * kseg, fr) << 4);
-  const uint8_t* p1 = sAB + fr * 128 + (slot_of(2 * kseg + 1, fr) << 4);
-  const v4f p = mfma_fp8(frag_at<0>(p0, p1), frag_at<2048>(p0, p1));
-  for (int v = 0; v < 4; ++v) C[(4 * kseg + v) * 16 + fr] = p[v];
-}
-
-extern "C" int moe_debug_mfma_probe(const void* A, const void* B, float* C, void* stream) {
-  if (!A || !B || !C) return kErrNullPointer;
-  if (!aligned16(A) || !aligned16(B)) return kErrBadShape;
-  hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
-                     (const uint8_t*)A, (const uint8_t*)B, C);
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

@@ -121,8 +121,9 @@ def test_chunked_and_mapped_entry_points_validate_arguments(L):
 
 def test_noalloc_align_checks_its_limit_before_any_device_call(L):
     """The allocation-free align rejects a problem whose workspace exceeds its
-    static array (MOE_ALIGN_NOALLOC_SCRATCH_BYTES) and bad sizes before it
-    touches a device, so these calls are safe without a GPU."""
+    static array (MOE_ALIGN_NOALLOC_SCRATCH_BYTES), bad sizes, expert counts,
+    block sizes, null pointers and short outputs before it touches a device,
+    so these calls are safe without a GPU."""
     text = HEADER.read_text()
     limit = int(eval(re.search(r"#define\s+MOE_ALIGN_NOALLOC_SCRATCH_BYTES\s+(\([^)]*\))", text).group(1)))
     assert limit == 4 * 1024 * 1024
@@ -132,4 +133,13 @@ def test_noalloc_align_checks_its_limit_before_any_device_call(L):
     assert _lib.STATUS[L.moe_align_block_size_noalloc(p, S, E, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_CAPACITY"
     assert _lib.STATUS[L.moe_align_block_size_noalloc(p, -1, E, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_BAD_SHAPE"
     assert _lib.STATUS[L.moe_align_block_size_noalloc(p, 64, 0, 128, p, p, p, 1 << 30, None)] == "MOE_ERR_BAD_EXPERTS"
+    # the remaining argument checks also run before the symbol lookup
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, 64, 2000, 128, p, p, p, 1 << 30, None)] == \
+        "MOE_ERR_BAD_EXPERTS"
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, 64, 8, 48, p, p, p, 1 << 30, None)] == \
+        "MOE_ERR_BAD_BLOCK_SIZE"
+    for nulls in ((None, p, p, p), (p, None, p, p), (p, p, None, p), (p, p, p, None)):
+        assert _lib.STATUS[L.moe_align_block_size_noalloc(nulls[0], 64, 8, 16, nulls[1], nulls[2], nulls[3],
+                                                          1 << 20, None)] == "MOE_ERR_NULL_POINTER"
+    assert _lib.STATUS[L.moe_align_block_size_noalloc(p, 64, 8, 16, p, p, p, 64, None)] == "MOE_ERR_CAPACITY"
 

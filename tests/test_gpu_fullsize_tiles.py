@@ -1,11 +1,15 @@
-"""GPU: whole output tiles of the full-size DeepSeek-V3 and Mixtral layers
-against the CPU oracle.
+"""GPU: whole output tiles of the full-size DeepSeek-V3, Mixtral, Qwen3 and
+DeepSeek-V3 decode layers against the CPU oracle.
 
 The layers are too large for the oracle to run whole, so the check picks
 complete workgroup tiles of each grouped GEMM launch (tests/tile_map.py):
 the first and last active tile of every XCD's range of the expert-major
-order, and both parts of a run split unevenly over its row tiles (a one-block
-tile and the larger last tile holding the run's padding).  For each picked
+order, both parts of a run split unevenly over its row tiles (a one-block
+tile and the larger last tile holding the run's padding), a tile of an expert
+with a single row tile (at the decode layer's 32-row tiles, two workgroups
+per CU, the weights of such an expert stream with the non-temporal hint), a
+256-row tile run by the 128-row body, and the first and last row tiles of the
+expert with the most blocks.  For each picked
 tile every valid row and every column of its n-tile is compared:
 * W13 as a plain GEMM (C13 bf16 by slot) with the accumulation bound of the
   GEMM tests, |d| <= 2^-7 |ref| + 2^-12 L1 (overlap/kernels.py:95-214);
@@ -32,7 +36,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=["dsv3", "mixtral", "qwen3"])
+@pytest.fixture(scope="module", params=["dsv3", "mixtral", "qwen3", "dsv3_decode"])
 def layer(request):
     from td_benchmark_amd import ops, workloads
     wl = workloads.CONFIGS[request.param]

@@ -28,34 +28,6 @@ def _log(msg: str) -> None:
     print(msg, flush=True)
 
 
-# ---------------------------------------------------------------- MFMA layout
-
-def test_mfma_probe_layout_matches_matmul():
-    from td_benchmark_amd._lib import check, lib
-    import ctypes
-    rng = np.random.default_rng(1)
-    codes = np.arange(256, dtype=np.uint8)
-    finite = codes[(codes & 0x7F) != 0x7F]
-    A = rng.choice(finite, size=(16, 128)).astype(np.uint8)
-    B = rng.choice(finite, size=(16, 128)).astype(np.uint8)
-    lut = oracle.e4m3_lut().astype(np.float64)
-    ref = lut[A] @ lut[B].T
-    dA = torch.from_numpy(A).cuda()
-    dB = torch.from_numpy(B).cuda()
-    dC = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
-    _log("mfma probe 16x16x128")
-    check(lib().moe_debug_mfma_probe(ctypes.c_void_p(dA.data_ptr()), ctypes.c_void_p(dB.data_ptr()),
-                                     ctypes.c_void_p(dC.data_ptr()), None), "probe")
-    torch.cuda.synchronize()
-    got = dC.cpu().numpy().astype(np.float64)
-    # Pairing/layout errors would move results by O(L1); the hardware's own
-    # reduced-precision accumulation stays within oracle.MFMA_L1_REL of L1.
-    l1 = np.abs(lut[A]) @ np.abs(lut[B]).T
-    err = np.abs(got - ref)
-    print(f"probe max err/L1 = {(err / l1).max():.3e}", flush=True)
-    assert np.all(err <= oracle.MFMA_L1_REL * l1)
-
-
 # ---------------------------------------------------------------- A1 quant
 
 @pytest.mark.parametrize("T,H,scale", [(1, 128, 1.0), (7, 256, 1.0), (64, 7168, 1.0),

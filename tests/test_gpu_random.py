@@ -42,7 +42,7 @@ def gemm_cases(draw):
     T = draw(st.integers(1, 200))
     H = 128 * draw(st.integers(1, 4))
     I = 128 * draw(st.integers(1, 3))
-    BM = draw(st.sampled_from([16, 32, 64, 128]))
+    BM = draw(st.sampled_from([16, 32, 64, 128, 256]))
     tile_m = draw(st.sampled_from([0] + [t for t in (16, 32, 64, 128, 256) if t >= BM]))
     hot = draw(st.integers(0, E - 1))
     skew = draw(st.floats(0.0, 0.9))
@@ -112,7 +112,7 @@ def test_random_w13_plain_and_w2_routed_gemms_within_the_bound(case):
 def layer_cases(draw):
     E = draw(st.integers(1, 32))
     return dict(T=draw(st.integers(1, 160)), H=128 * draw(st.integers(1, 4)), I=128 * draw(st.integers(1, 3)),
-                E=E, k=draw(st.integers(1, min(8, E))), BM=draw(st.sampled_from([16, 32, 64, 128])),
+                E=E, k=draw(st.integers(1, min(8, E))), BM=draw(st.sampled_from([16, 32, 64, 128, 256])),
                 routing=draw(st.sampled_from(["softmax", "sigmoid"])), seed=draw(st.integers(0, 10**6)))
 
 
@@ -196,7 +196,7 @@ def test_long_k_plain_gemms_within_the_bound(which):
 @st.composite
 def fused_cases(draw):
     E = draw(st.integers(1, 24))
-    BM = draw(st.sampled_from([16, 32, 64, 128]))
+    BM = draw(st.sampled_from([16, 32, 64, 128, 256]))
     return dict(T=draw(st.integers(1, 160)), H=128 * draw(st.integers(1, 4)), I=128 * draw(st.integers(1, 3)),
                 E=E, k=draw(st.integers(1, min(8, E))), BM=BM,
                 tile_m=draw(st.sampled_from([0] + [t for t in (16, 32, 64, 128, 256) if t >= BM])),

@@ -26,8 +26,11 @@ from moe_cases import bf16_bits, dequant_weights_f32, make_case, to_gpu, u8_bits
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
-# (T, H, I, E, k, BM, n_gateup, n_down): 32-row tiles; and S >= 160*E (256-row tiles over 64-row blocks)
-CASES = {"short": (150, 512, 384, 6, 3, 32, 4, 2), "tall": (700, 512, 256, 4, 2, 64, 2, 4)}
+# (T, H, I, E, k, BM, n_gateup, n_down): 32-row tiles; S >= 160*E (256-row tiles over 64-row blocks);
+# and 256-row blocks whose experts' second tiles hold 90, 91, 47 and 92 valid rows (the 128-row and
+# 64-row bodies of a 256-row launch, with the K-split accumulate epilogue)
+CASES = {"short": (150, 512, 384, 6, 3, 32, 4, 2), "tall": (700, 512, 256, 4, 2, 64, 2, 4),
+         "body128": (672, 512, 256, 4, 2, 256, 2, 4)}
 
 
 @pytest.mark.parametrize("name", sorted(CASES))

@@ -80,9 +80,14 @@ def tile_map(eids: np.ndarray, ntpp: int, bma: int, tile_m: int, n_tiles: int,
 
 def pick_tiles(tiles: list[TileInfo], sorted_ids: np.ndarray, S: int, tail_rows: int = 64) -> dict[str, TileInfo]:
     """Named tiles worth checking whole: the first and last active tile of each
-    XCD range, a tile short enough for the tail body, and both parts of a run
+    XCD range, a tile short enough for the tail body, both parts of a run
     split unevenly over its row tiles (the smaller first part -- one block
-    when a 3-block run is split 1 + 2 -- and the larger last part)."""
+    when a 3-block run is split 1 + 2 -- and the larger last part), a tile of
+    an expert with a single row tile (16- and 32-row launches load its
+    weights with the non-temporal hint), a 256-row tile whose valid rows fit
+    the 128-row body but not the 64-row one, and the first row tile (first
+    n-tile) and last row tile (last n-tile) of the expert with the most
+    blocks."""
     out: dict[str, TileInfo] = {}
     by_xcd: dict[int, list[TileInfo]] = {}
     for ti in tiles:
@@ -104,6 +109,21 @@ def pick_tiles(tiles: list[TileInfo], sorted_ids: np.ndarray, S: int, tail_rows:
         if ti.expert >= 0 and "long_of_split" not in out and ti.units > 1 and ti.run_blocks % ti.units \
                 and ti.u == ti.units - 1:
             out["long_of_split"] = ti
+        if ti.expert >= 0 and "single_row_tile" not in out and ti.units == 1:
+            out["single_row_tile"] = ti
+        if ti.expert >= 0 and "body128_of_256" not in out and ti.rows > 128 and tail_rows < nvalid(ti) <= 128:
+            out["body128_of_256"] = ti
+    live = [ti for ti in tiles if ti.expert >= 0]
+    if live:
+        hot = max(live, key=lambda a: (a.run_blocks, -a.t))
+        n_tiles = max(ti.j for ti in tiles) + 1
+        run_tiles = [ti for ti in live if ti.expert == hot.expert and ti.run_blocks == hot.run_blocks]
+        first = [ti for ti in run_tiles if ti.u == 0 and ti.j == 0]
+        last = [ti for ti in run_tiles if ti.u == ti.units - 1 and ti.j == n_tiles - 1]
+        if first:
+            out["hot_first"] = first[0]
+        if last:
+            out["hot_last"] = last[0]
     return out
 
 
