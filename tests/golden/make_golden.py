@@ -6,8 +6,8 @@ N(0, 0.02) quantised 128x128).  Expected outputs: every intermediate of the
 stage chain computed by the CPU oracle with the reference's rounding points
 (quant codes/scales, align outputs, C13, h, intermediate codes/scales, D, y),
 the fp32 golden of verify.py:14-47, the calibrated absolute tolerance of
-tests/calibrate_tolerance.py, and the oracle's L1 magnitudes for the two GEMMs
-(the GPU parity tests' accumulation bound).
+tests/calibrate_tolerance.py, and the oracle's L1 magnitudes and matrix-core
+bounds for the two GEMMs (the GPU parity tests' accumulation bound).
 
 The reference itself cannot be imported here (it needs vLLM and a GPU
 runtime for its MoE path), so the fixture freezes this build's pinned oracle:
@@ -38,11 +38,12 @@ SHAPE = dict(T=32, H=256, I=128, E=4, k=2, BM=16)
 def build_fixture() -> dict[str, np.ndarray]:
     c = make_case(**SHAPE, seed=0, routing="softmax")
     st = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, c.BM)
-    _, mag13 = oracle.grouped_gemm(st["q1"], st["s1"], c.w13_q, c.w13_s, st["sorted_ids"],
-                                   st["expert_ids"], st["ntpp"], c.BM, c.S, c.k, with_magnitude=True)
-    _, mag2 = oracle.grouped_gemm(st["q2"], st["s2"], c.w2_q, c.w2_s, st["sorted_ids"],
-                                  st["expert_ids"], st["ntpp"], c.BM, c.S, 1,
-                                  topk_w=c.topk_w.ravel(), with_magnitude=True)
+    _, mag13, bound13 = oracle.grouped_gemm(st["q1"], st["s1"], c.w13_q, c.w13_s, st["sorted_ids"],
+                                            st["expert_ids"], st["ntpp"], c.BM, c.S, c.k, with_magnitude=True,
+                                            with_bound=True)
+    _, mag2, bound2 = oracle.grouped_gemm(st["q2"], st["s2"], c.w2_q, c.w2_s, st["sorted_ids"],
+                                          st["expert_ids"], st["ntpp"], c.BM, c.S, 1,
+                                          topk_w=c.topk_w.ravel(), with_magnitude=True, with_bound=True)
     w1 = dequant_weights_f32(c.w13_q, c.w13_s)
     w2 = dequant_weights_f32(c.w2_q, c.w2_s)
     x = oracle.bf16_to_f32(c.x)
@@ -55,8 +56,8 @@ def build_fixture() -> dict[str, np.ndarray]:
         "q1": st["q1"], "s1": st["s1"],
         "sorted_ids": st["sorted_ids"], "expert_ids": st["expert_ids"],
         "ntpp": np.array([st["ntpp"]], np.int32),
-        "c13": st["c13"], "mag13": mag13, "h": st["h"], "q2": st["q2"], "s2": st["s2"],
-        "D": st["D"], "mag2": mag2, "y": st["y"],
+        "c13": st["c13"], "mag13": mag13, "bound13": bound13, "h": st["h"], "q2": st["q2"], "s2": st["s2"],
+        "D": st["D"], "mag2": mag2, "bound2": bound2, "y": st["y"],
         "golden": golden, "atol": np.array([atol], np.float64),
     }
 

@@ -44,7 +44,8 @@ def test_oracle_reproduces_fixture(fixture):
     for key in EXACT:
         assert np.array_equal(fresh[key], fixture[key]), key
     np.testing.assert_allclose(fresh["golden"], fixture["golden"], rtol=1e-5, atol=1e-7)
-    np.testing.assert_allclose(fresh["mag13"], fixture["mag13"], rtol=1e-6)
+    for key in ("mag13", "mag2", "bound13", "bound2"):
+        np.testing.assert_allclose(fresh[key], fixture[key], rtol=1e-6)
     np.testing.assert_allclose(fresh["atol"], fixture["atol"], rtol=1e-4)
 
 

@@ -3,8 +3,10 @@ C ABI (td_benchmark_amd.ops -> libmoe_mi355x.so).
 
 Bars: bit-exact for the integer/byte stages (align, quant codes and scales,
 top-k reduce given identical inputs); FP8 codes of the fused intermediate
-within 1 e4m3 ULP on <= 0.1% of codes; bf16 GEMM outputs within 1 bf16 ULP
-(the kernel and the oracle both accumulate fp32 but in different orders).
+held to the A7 account (every difference traced to the matrix core's
+truncation; the north-star rate reported); bf16 GEMM outputs within one bf16
+step plus the oracle's matrix-core bound (its measured in-instruction
+truncation and the fp32 roundings of both scale chains).
 """
 from __future__ import annotations
 
@@ -174,9 +176,9 @@ GEMM_CASES = [
 ]
 
 
-def _gemm_close(got: np.ndarray, ref: np.ndarray, mag: np.ndarray):
-    bad = oracle.gemm_close(got, ref, mag)
-    assert bad.sum() == 0, f"{bad.sum()} of {bad.size} outputs outside 1 bf16 ulp + MFMA L1 bound"
+def _gemm_close(got: np.ndarray, ref: np.ndarray, bound: np.ndarray):
+    bad = oracle.gemm_close(got, ref, bound)
+    assert bad.sum() == 0, f"{bad.sum()} of {bad.size} outputs outside 1 bf16 ulp + the matrix-core bound"
 
 
 def _bf16_close(got: np.ndarray, ref: np.ndarray, ulps: int = 1):
@@ -193,8 +195,8 @@ def test_grouped_gemm_w13_plain(T, H, I, E, k, BM, routing):
     c = make_case(T, H, I, E, k, BM, seed=T + H, routing=routing)
     q1, s1 = oracle.quant_group128(c.x)
     sorted_ids, eids, ntpp = oracle.moe_align(c.topk_ids, E, BM)
-    ref, mag = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
-                                   with_magnitude=True)
+    ref, bnd = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
+                                   with_bound=True)
     g = to_gpu(c)
     _log(f"gemm w13 plain T={T} H={H} I={I} E={E} k={k} BM={BM}")
     dq = torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn)
@@ -206,7 +208,7 @@ def test_grouped_gemm_w13_plain(T, H, I, E, k, BM, routing):
     ops.dispatch_fused_moe_kernel(dq, g["w13"], C, ds, g["w13_s"], None, None, d_sorted, d_eids, d_ntpp,
                                   False, k, {"BLOCK_SIZE_M": BM}, block_shape=[128, 128])
     torch.cuda.synchronize()
-    _gemm_close(bf16_bits(C).reshape(c.S, 2 * I), ref, mag)
+    _gemm_close(bf16_bits(C).reshape(c.S, 2 * I), ref, bnd)
 
 
 @pytest.mark.parametrize("T,H,I,E,k,BM,routing", GEMM_CASES)
@@ -253,10 +255,10 @@ def test_w13_fused_silu_quant(T, H, I, E, k, BM, routing):
     assert (h_np != h_ref).mean() <= 1e-3
     # 4) against the all-CPU chain (exact dots): every differing code traced to
     #    a differing h or group scale, each differing h to its C13 inputs, each
-    #    C13 flip inside the MFMA accumulation bound, and the measured rate
+    #    C13 flip inside the matrix core's accumulation bound, and the measured rate
     #    (the north-star rate is reported beside it)
     rep = a7_account(hq_np, hs_np, h_np[slots], bf16_bits(C)[slots], st["q2"][slots], st["s2"][slots],
-                     st["h"][slots], st["c13"][slots], st["c13_f32"][slots], st["mag13"][slots])
+                     st["h"][slots], st["c13"][slots], st["c13_f32"][slots], st["bound13"][slots])
     a7_assert(rep, f"w13 fused T={T} H={H} I={I} E={E} k={k} BM={BM}")
 
 
@@ -271,8 +273,8 @@ def test_grouped_gemm_w2_routed(T, H, I, E, k, BM, routing):
     hq = rng.integers(0, 256, size=(mp, I), dtype=np.uint8)
     hq[(hq & 0x7F) == 0x7F] = 0
     hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
-    ref, mag = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
-                                   a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_magnitude=True)
+    ref, bnd = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
+                                   a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_bound=True)
     g = to_gpu(c)
     _log(f"gemm w2 T={T} H={H} I={I} E={E} k={k} BM={BM}")
     D = torch.zeros((c.S, 1, H), dtype=torch.bfloat16, device="cuda")
@@ -282,7 +284,7 @@ def test_grouped_gemm_w2_routed(T, H, I, E, k, BM, routing):
                                   torch.tensor([ntpp], dtype=torch.int32, device="cuda"), True, 1,
                                   {"BLOCK_SIZE_M": BM}, a_by_pos=True)
     torch.cuda.synchronize()
-    _gemm_close(bf16_bits(D).reshape(c.S, H), ref, mag)
+    _gemm_close(bf16_bits(D).reshape(c.S, H), ref, bnd)
 
 
 def test_grouped_gemm_expert_minus_one_writes_zeros():
@@ -353,8 +355,8 @@ def test_grouped_gemm_runs_longer_than_65_blocks(tile_m):
     runs = [n for _, n in runs_of(eids[: ntpp // BM])]
     assert max(runs) > 65, runs
     _log(f"long runs {runs} tile_m={tile_m}")
-    ref, mag = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
-                                   with_magnitude=True)
+    ref, bnd = oracle.grouped_gemm(q1, s1, c.w13_q, c.w13_s, sorted_ids, eids, ntpp, BM, c.S, k,
+                                   with_bound=True)
     g = to_gpu(c)
     dq = torch.from_numpy(q1).cuda().view(torch.float8_e4m3fn)
     ds = torch.from_numpy(s1).cuda()
@@ -370,12 +372,12 @@ def test_grouped_gemm_runs_longer_than_65_blocks(tile_m):
     hq = rng.integers(0, 256, size=(mp, I), dtype=np.uint8)
     hq[(hq & 0x7F) == 0x7F] = 0
     hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
-    ref2, mag2 = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
-                                     a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_magnitude=True)
+    ref2, bnd2 = oracle.grouped_gemm(hq, hs, c.w2_q, c.w2_s, sorted_ids, eids, ntpp, BM, c.S, 1,
+                                     a_row_by_pos=True, topk_w=c.topk_w.ravel(), with_bound=True)
     D = torch.zeros((c.S, H), dtype=torch.bfloat16, device="cuda")
     ops.dispatch_fused_moe_kernel(torch.from_numpy(hq).cuda().view(torch.float8_e4m3fn), g["w2"], D,
                                   torch.from_numpy(hs).cuda(), g["w2_s"], None, g["topk_w"].view(-1), d_sorted,
                                   d_eids, d_ntpp, True, 1, {"BLOCK_SIZE_M": BM}, a_by_pos=True, tile_m=tile_m)
     torch.cuda.synchronize()
-    _gemm_close(bf16_bits(C), ref, mag)
-    _gemm_close(bf16_bits(D), ref2, mag2)
+    _gemm_close(bf16_bits(C), ref, bnd)
+    _gemm_close(bf16_bits(D), ref2, bnd2)

@@ -101,7 +101,7 @@ def test_layer_parity(T, H, I, E, k, BM, routing):
     ops.silu_and_mul(h, C)
     torch.cuda.synchronize()
     rep4 = a7_account(hq_slot, hs_slot, bf16_bits(h), bf16_bits(C), st["q2"], st["s2"], st["h"], st["c13"],
-                      st["c13_f32"], st["mag13"])
+                      st["c13_f32"], st["bound13"])
     a7_assert(rep4, f"layer T={T} H={H} I={I} E={E} k={k} BM={BM} {routing}")
 
 

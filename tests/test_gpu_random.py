@@ -85,26 +85,26 @@ def test_random_w13_plain_and_w2_routed_gemms_within_the_bound(case):
     cfg = {"BLOCK_SIZE_M": BM}
 
     # W13, plain epilogue, A rows by token
-    ref, mag = oracle.grouped_gemm(q1, s1, w13, w13_s, srt, eids, ntpp, BM, S, k, with_magnitude=True)
+    ref, bnd = oracle.grouped_gemm(q1, s1, w13, w13_s, srt, eids, ntpp, BM, S, k, with_bound=True)
     C = torch.zeros((T, k, 2 * I), dtype=torch.bfloat16, device="cuda")
     ops.dispatch_fused_moe_kernel(_gpu(q1, torch.float8_e4m3fn), _gpu(w13, torch.float8_e4m3fn), C, _gpu(s1),
                                   _gpu(w13_s), None, None, d_srt, d_eids, d_ntpp, False, k, cfg, tile_m=tm)
     torch.cuda.synchronize()
-    bad = oracle.gemm_close(bf16_bits(C).reshape(S, 2 * I), ref, mag)
+    bad = oracle.gemm_close(bf16_bits(C).reshape(S, 2 * I), ref, bnd)
     assert not bad.any(), f"W13: {int(bad.sum())} of {bad.size} outside the bound"
 
     # W2, A rows by sorted position, routed weights
     mp = srt.size
     hq = _fp8_codes(rng, (mp, I))
     hs = (rng.random((mp, I // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
-    ref2, mag2 = oracle.grouped_gemm(hq, hs, w2, w2_s, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
-                                     topk_w=w.ravel(), with_magnitude=True)
+    ref2, bnd2 = oracle.grouped_gemm(hq, hs, w2, w2_s, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
+                                     topk_w=w.ravel(), with_bound=True)
     D = torch.zeros((S, 1, H), dtype=torch.bfloat16, device="cuda")
     ops.dispatch_fused_moe_kernel(_gpu(hq, torch.float8_e4m3fn), _gpu(w2, torch.float8_e4m3fn), D, _gpu(hs),
                                   _gpu(w2_s), None, _gpu(w.ravel()), d_srt, d_eids, d_ntpp, True, 1, cfg,
                                   a_by_pos=True, tile_m=tm)
     torch.cuda.synchronize()
-    bad = oracle.gemm_close(bf16_bits(D).reshape(S, H), ref2, mag2)
+    bad = oracle.gemm_close(bf16_bits(D).reshape(S, H), ref2, bnd2)
     assert not bad.any(), f"W2: {int(bad.sum())} of {bad.size} outside the bound"
 
 
@@ -175,21 +175,21 @@ def test_long_k_plain_gemms_within_the_bound(which):
     if which == "w13_plain":
         x = oracle.f32_to_bf16(rng.standard_normal((T, K), dtype=np.float32))
         A, As = oracle.quant_group128(x)
-        ref, mag = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, k, with_magnitude=True)
+        ref, bnd = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, k, with_bound=True)
         C = torch.zeros((T, k, N), dtype=torch.bfloat16, device="cuda")
         ops.dispatch_fused_moe_kernel(_gpu(A, torch.float8_e4m3fn), _gpu(B, torch.float8_e4m3fn), C, _gpu(As),
                                       _gpu(Bs), None, None, d_srt, d_eids, d_ntpp, False, k, {"BLOCK_SIZE_M": BM})
     else:
         A = _fp8_codes(rng, (srt.size, K))
         As = (rng.random((srt.size, K // 128), dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
-        ref, mag = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
-                                       topk_w=w.ravel(), with_magnitude=True)
+        ref, bnd = oracle.grouped_gemm(A, As, B, Bs, srt, eids, ntpp, BM, S, 1, a_row_by_pos=True,
+                                       topk_w=w.ravel(), with_bound=True)
         C = torch.zeros((S, 1, N), dtype=torch.bfloat16, device="cuda")
         ops.dispatch_fused_moe_kernel(_gpu(A, torch.float8_e4m3fn), _gpu(B, torch.float8_e4m3fn), C, _gpu(As),
                                       _gpu(Bs), None, _gpu(w.ravel()), d_srt, d_eids, d_ntpp, True, 1,
                                       {"BLOCK_SIZE_M": BM}, a_by_pos=True)
     torch.cuda.synchronize()
-    bad = oracle.gemm_close(bf16_bits(C).reshape(S, N), ref, mag)
+    bad = oracle.gemm_close(bf16_bits(C).reshape(S, N), ref, bnd)
     assert not bad.any(), f"{which}: {int(bad.sum())} of {bad.size} outside the bound"
 
 
@@ -236,5 +236,5 @@ def test_random_fused_w13_equals_the_unfused_chain(case):
     assert np.array_equal(hs_np.view(np.uint32), s2.cpu().numpy()[slots].view(np.uint32))
     st_ = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, BM)
     rep = a7_account(hq_np, hs_np, bf16_bits(h)[slots], bf16_bits(C)[slots], st_["q2"][slots], st_["s2"][slots],
-                     st_["h"][slots], st_["c13"][slots], st_["c13_f32"][slots], st_["mag13"][slots])
+                     st_["h"][slots], st_["c13"][slots], st_["c13_f32"][slots], st_["bound13"][slots])
     a7_assert(rep, f"random fused W13 {case}")
