@@ -15,6 +15,9 @@
  *   2  four v_mfma_f32_16x16x32_fp8_fp8 from zero, summed by fp32 adds
  *   3  four 16x16x128 f8f6f4 instructions, each with only one 32-element
  *      quarter of K non-zero, summed by fp32 adds
+ *   4  the codes converted to bf16 (exactly) and four
+ *      v_mfma_f32_16x16x32_bf16, the accumulator chained through the
+ *      instruction
  */
 #ifndef MOE_PROBE_H
 #define MOE_PROBE_H

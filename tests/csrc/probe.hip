@@ -24,9 +24,33 @@ __device__ __forceinline__ v8i only_quarter(const v8i& f, int q) {
   return r;
 }
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// The 8 FP8 codes of quarter q as bf16 (exact: every e4m3 value is a bf16).
+__device__ __forceinline__ v8bf quarter_bf16(const v8i& f, int q) {
+  const int lo = f[2 * q], hi = f[2 * q + 1];
+  v8bf r;
+  r[0] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 0);
+  r[1] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 1);
+  r[2] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 2);
+  r[3] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 3);
+  r[4] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 0);
+  r[5] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 1);
+  r[6] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 2);
+  r[7] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 3);
+  return r;
+}
+
 __device__ __forceinline__ v4f dot_form(const v8i& a, const v8i& b, int form) {
   const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
   if (form == 0) return mfma_fp8(a, b);
+  if (form == 4) {
+    v4f acc = zero;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(quarter_bf16(a, q), quarter_bf16(b, q), acc, 0, 0, 0);
+    return acc;
+  }
   v4f acc = zero;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -134,7 +158,7 @@ using namespace moe_probe;
 
 extern "C" int moe_probe_mfma_dot(const void* A, const void* B, float* C, int64_t n, int32_t form, void* stream) {
   if (!A || !B || !C) return kErrNullPointer;
-  if (n <= 0 || n > (1 << 20) || form < 0 || form > 3) return kErrBadShape;
+  if (n <= 0 || n > (1 << 20) || form < 0 || form > 4) return kErrBadShape;
   if (((uintptr_t)A & 15) || ((uintptr_t)B & 15)) return kErrBadShape;
   hipLaunchKernelGGL(dot_kernel, dim3((unsigned)n), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)A,
                      (const uint8_t*)B, C, (int)form);
@@ -144,7 +168,7 @@ extern "C" int moe_probe_mfma_dot(const void* A, const void* B, float* C, int64_
 extern "C" int moe_probe_block_gemm(const void* A, const float* As, const void* B, const float* Bs, int64_t M,
                                     int64_t N, int64_t K, int32_t form, void* C, void* stream) {
   if (!A || !As || !B || !Bs || !C) return kErrNullPointer;
-  if (M <= 0 || N <= 0 || K <= 0 || M % 16 || N % 16 || K % 128 || form < 0 || form > 3) return kErrBadShape;
+  if (M <= 0 || N <= 0 || K <= 0 || M % 16 || N % 16 || K % 128 || form < 0 || form > 4) return kErrBadShape;
   if (M / 16 > 65535 || N / 16 > (int64_t)1 << 30) return kErrBadShape;
   if (((uintptr_t)A & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 7)) return kErrBadShape;
   hipLaunchKernelGGL(block_gemm_kernel, dim3((unsigned)(N / 16), (unsigned)(M / 16)), dim3(64), 0,
@@ -155,7 +179,7 @@ extern "C" int moe_probe_block_gemm(const void* A, const float* As, const void* 
 
 extern "C" int moe_probe_mfma_rate(int64_t waves, int32_t iters, int32_t form, float* sink, void* stream) {
   if (!sink) return kErrNullPointer;
-  if (waves <= 0 || waves % 4 || waves > (1 << 22) || iters <= 0 || form < 0 || form > 3) return kErrBadShape;
+  if (waves <= 0 || waves % 4 || waves > (1 << 22) || iters <= 0 || form < 0 || form > 4) return kErrBadShape;
   hipLaunchKernelGGL(rate_kernel, dim3((unsigned)(waves / 4)), dim3(256), 0, (hipStream_t)stream, (int)iters,
                      (int)form, sink);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;

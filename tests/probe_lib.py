@@ -25,8 +25,10 @@ FORM_K128 = 0          # one 16x16x128 f8f6f4 (the grouped GEMM's form)
 FORM_K32_CHAINED = 1   # four 16x16x32, accumulator chained through the instruction
 FORM_K32_FP32 = 2      # four 16x16x32 from zero, fp32 adds
 FORM_K128_QUARTERS = 3 # four 16x16x128 with one K quarter each, fp32 adds
-FORMS = {FORM_K128: "16x16x128", FORM_K32_CHAINED: "4x16x16x32 chained",
-         FORM_K32_FP32: "4x16x16x32 + fp32 adds", FORM_K128_QUARTERS: "4x16x16x128 quarters + fp32 adds"}
+FORM_BF16 = 4          # codes converted to bf16, four 16x16x32 bf16 MFMAs chained
+FP8_FORMS = {FORM_K128: "16x16x128", FORM_K32_CHAINED: "4x16x16x32 chained",
+             FORM_K32_FP32: "4x16x16x32 + fp32 adds", FORM_K128_QUARTERS: "4x16x16x128 quarters + fp32 adds"}
+FORMS = {**FP8_FORMS, FORM_BF16: "bf16 4x16x16x32"}
 
 _lib: ctypes.CDLL | None = None
 

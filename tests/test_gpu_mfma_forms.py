@@ -3,9 +3,10 @@ test-only probe library (tests/csrc, moe_probe.h), which runs the grouped
 GEMM's own fragment code (td_benchmark_amd/csrc/mfma_frag.hpp).
 
 What the structured probes establish about one 128-element FP8 dot (the same
-for every instruction form measured: one 16x16x128 f8f6f4, four 16x16x32
+for every FP8 instruction form measured: one 16x16x128 f8f6f4, four 16x16x32
 chained through the accumulator or summed in fp32, four quarter-masked
-16x16x128):
+16x16x128; a fifth form, the codes converted to bf16 and four bf16 16x16x32
+MFMAs, is measured beside them):
 * the products are summed in 16 groups of 8 consecutive K (K as the GEMM
   lays it out: lane kseg holds K bytes [32 kseg, 32 kseg + 32) of its row);
 * inside a group every product is truncated toward zero on the grid
@@ -101,7 +102,7 @@ def _zeros(n: int) -> tuple[np.ndarray, np.ndarray]:
     return np.zeros((n, 16, 128), np.uint8), np.zeros((n, 16, 128), np.uint8)
 
 
-@pytest.mark.parametrize("form", sorted(probe_lib.FORMS))
+@pytest.mark.parametrize("form", sorted(probe_lib.FP8_FORMS))
 def test_dot_model_structure(form):
     name = probe_lib.FORMS[form]
     # groups: a product of 2^8 at K position a and one of 2^-9 at b; the small
@@ -257,6 +258,11 @@ def test_a7_codes_by_dot_form():
             if form == probe_lib.FORM_K128:
                 a7_assert(rep, f"A7 by dot form, seed {seed}, {name}")
                 assert c13_same >= 0.9999 and code_same >= 0.9999, (c13_same, code_same)
+            elif form == probe_lib.FORM_BF16:
+                # the bf16 path: every difference still traced to C13, and
+                # fewer flips than the FP8 forms' truncation causes
+                assert rep["untraced"] == 0 and rep["bad_scale"] == 0, rep
+                assert rep.get("c13_flip_need_max_bound", 0.0) <= 1.0, rep
             else:
                 # the other forms answer to the same causes
                 assert rep["untraced"] == 0 and rep["bad_scale"] == 0, rep
