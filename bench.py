@@ -16,7 +16,9 @@ region.  ``roofline`` describes the dominant kernel (the W13 GEMM).
 golden path (restated in oracle/golden_torch.py, all host cores) on a bounded
 sample of the same workload.  ``shared_expert`` times the shared expert (one
 E=1, top-1 expert of the same hidden and intermediate size) on the layer's own
-FP8 input, outside the layer time.
+FP8 input, outside the layer time.  ``power`` gives socket power, graphics
+clock and energy per call of the layer, W13 and W2, each run back to back
+for a few seconds (amd-smi; null where it is unavailable).
 """
 from __future__ import annotations
 
@@ -150,6 +152,68 @@ def shared_expert_leg(runner, wl, steps: int, warmup: int) -> dict:
             "input": "the routed layer's FP8 activations and 1x128 scales (no second quant)"}
 
 
+def _amd_smi_sample() -> tuple[float, float] | None:
+    """(socket power W, mean graphics clock MHz over the XCDs) of GPU 0 from
+    `amd-smi metric -p -c --json -g 0`; None when amd-smi is unavailable."""
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json", "-g", "0"], capture_output=True,
+                             text=True, timeout=10).stdout
+        doc, _ = json.JSONDecoder().raw_decode(out[out.index("{"):])
+        gpu = doc["gpu_data"][0] if "gpu_data" in doc else doc
+        power = float(gpu["power"]["socket_power"]["value"])
+        clks = [float(v["clk"]["value"]) for k, v in gpu["clock"].items()
+                if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+        return power, sum(clks) / len(clks)
+    except (OSError, ValueError, KeyError, TypeError, IndexError, ZeroDivisionError,
+            subprocess.SubprocessError):
+        return None
+
+
+def power_leg(fn, seconds: float) -> dict | None:
+    """Runs ``fn`` back to back for about ``seconds`` while a thread samples
+    socket power and the graphics clock with amd-smi; returns the averages of
+    the samples taken after the first half second, the calls' mean time and
+    the energy per call (power x time).  None without amd-smi."""
+    import threading
+    import torch
+    if _amd_smi_sample() is None:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            smp = _amd_smi_sample()
+            if smp is not None and time.perf_counter() - t0 > 0.5:
+                samples.append(smp)
+            stop.wait(0.2)
+
+    fn()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_end = time.perf_counter() + seconds
+    calls = 0
+    start.record()
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            fn()
+        calls += 20
+        torch.cuda.synchronize()
+    end.record()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    if not samples:
+        return None
+    us = start.elapsed_time(end) * 1e3 / calls
+    power = sum(p for p, _ in samples) / len(samples)
+    return {"us_per_call": us, "socket_power_W": power, "gfx_clock_MHz": sum(c for _, c in samples) / len(samples),
+            "energy_J_per_call": power * us * 1e-6, "samples": len(samples), "calls": calls}
+
+
 def _time_cpu(fn, warmup: int, repeat: int) -> dict:
     """bench_cpu semantics (moe_bench/timing.py:37-45): warmup calls, then
     ``repeat`` timed calls with time.perf_counter."""
@@ -249,6 +313,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shared", action="store_true",
                     help="skip the shared-expert leg (one E=1, top-1 expert on the layer's FP8 input)")
+    ap.add_argument("--power-seconds", type=float, default=2.0,
+                    help="seconds of back-to-back layer, W13 and W2 runs sampled for socket power and clock "
+                         "(0 to skip)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the multi-GPU expert/tensor-parallel "
@@ -436,6 +503,12 @@ def main() -> int:
         "active_experts": active,
         "roofline": roof,
     }
+    if args.power_seconds > 0 and pipe is None:
+        result["power"] = {"layer": power_leg(lambda: step(), args.power_seconds),
+                           "w13": power_leg(runner.stage_w13, args.power_seconds),
+                           "w2": power_leg(lambda: runner.stage_w2(data.topk_w), args.power_seconds),
+                           "source": "amd-smi metric -p -c (socket power, mean gfx clock of the XCDs), "
+                                     "sampled every ~0.2 s while the stage runs back to back"}
     if not args.no_shared:
         result["shared_expert"] = shared_expert_leg(runner, wl, args.steps, args.warmup)
     if not args.no_cpu_baseline:
