@@ -41,10 +41,21 @@ extern "C" {
  * Replaces vLLM moe_kernel_quantize_input(A, None, float8_e4m3fn, False,
  * [128,128]) as called at overlap/overlap_forward.py:257-259 and :282-284
  * (arithmetic of verify.py:108-117).
- * x [T,H] bf16 -> q [T,H] e4m3fn, scales [T, H/128] fp32; H % 128 == 0,
- * x 16-byte aligned, q 8-byte aligned. */
+ * x [T,H] bf16 -> q [T,H] e4m3fn, scales [T, ceil(H/128)] fp32.  When H is
+ * not a multiple of 128 a row's last group holds H mod 128 values; the
+ * reference zero-pads it (verify.py:111-113), which changes neither its amax
+ * nor its codes.  x 2-byte aligned; H % 128 == 0 with x 16-byte and q 8-byte
+ * aligned takes the vectorised kernel. */
 int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void* q_fp8, float* scales,
                        void* stream);
+
+/* The same quant into rows of ldq >= ceil(H/128)*128 bytes, with the zero
+ * code in columns [H, ceil(H/128)*128): the quantised zero padding of
+ * verify.py:111-113, so that a GEMM over the padded width equals one over H
+ * (no counterpart in the reference: the layout of the layer runner for
+ * widths that are not a multiple of 128). */
+int moe_quant_group128_padded(const void* x_bf16, int64_t T, int64_t H, void* q_fp8, int64_t ldq,
+                              float* scales, void* stream);
 
 /* A2 -- 128x128 block FP8 weight quant (build time).
  * Replaces quantize_block128 (data/checkpoint.py:28-40).

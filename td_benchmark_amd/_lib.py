@@ -34,6 +34,7 @@ _i32 = ctypes.c_int32
 # name -> (restype, argtypes); must match include/moe_mi355x.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "moe_quant_group128": (ctypes.c_int, [_P, _i64, _i64, _P, _P, _P]),
+    "moe_quant_group128_padded": (ctypes.c_int, [_P, _i64, _i64, _P, _i64, _P, _P]),
     "moe_quant_block128": (ctypes.c_int, [_P, _i64, _i64, _i64, _P, _P, _P]),
     "moe_align_max_padded": (ctypes.c_int64, [_i64, _i32, _i32]),
     "moe_align_workspace_bytes": (ctypes.c_int64, [_i64, _i32]),

@@ -7,7 +7,8 @@
 // code = e4m3fn_RNE(clamp(x / scale, +-448)).
 //
 // quant_group128 is HBM-bound: 2 B in + 1 B out per element + 4 B of scale per
-// 128 elements.  Sixteen lanes own one 128-element group (16 B = 8 bf16 each),
+// 128 elements (widths that are not a multiple of 128, or unaligned rows, take
+// a general one-wave-per-group kernel instead).  Sixteen lanes own one 128-element group (16 B = 8 bf16 each),
 // so every wave reads 1 KiB and writes 512 B contiguously with 128-bit loads;
 // the group amax is a 16-lane xor-shuffle reduction.  Non-temporal
 // (streaming) loads and stores and a shallow per-thread unroll measured best
@@ -90,6 +91,36 @@ __global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(
   }
 }
 
+// Any width and row strides (the vectorised kernel above needs W % 128 == 0
+// and aligned rows): one wave per 128-column group of one row, two columns
+// per lane.  A row's last group holds W mod 128 columns when W is not a
+// multiple of 128; the reference zero-pads it to 128 (verify.py:111-113), and
+// zeros change neither the group's amax nor the other codes, so only the W
+// columns are read and their codes written.  Columns [W, pad_to) of q get the
+// zero code (the zero padding, quantised).
+__global__ __launch_bounds__(256) void quant_group128_any_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t rows, int64_t W, int64_t pad_to,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ s, int64_t lds) {
+  const int lane = threadIdx.x & 63;
+  const int64_t groups = (pad_to + 127) / 128;
+  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (row, group) of this wave
+  if (g >= rows * groups) return;
+  const int64_t r = g / groups, c0 = (g % groups) * 128 + 2 * lane;
+  float v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] = c0 + j < W ? bf16_to_f32(x[r * ldx + c0 + j]) : 0.0f;
+  float amax = fmaxf(fabsf(v[0]), fabsf(v[1]));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float sc = group_scale(amax);
+  const float inv = 1.0f / sc;
+  const uint32_t codes = pack4_e4m3(clamp_fp8(div_by(v[0], sc, inv)), clamp_fp8(div_by(v[1], sc, inv)), 0.0f, 0.0f);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (c0 + j < pad_to) q[r * ldq + c0 + j] = c0 + j < W ? (uint8_t)(codes >> (8 * j)) : 0;
+  if (lane == 0 && g % groups * 128 < W) s[r * lds + g % groups] = sc;
+}
+
 // One workgroup per 128x128 block of one expert.  w fp32 [E, N, K] row-major.
 __global__ __launch_bounds__(256) void quant_block128_kernel(
     const float* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ s,
@@ -144,13 +175,27 @@ __global__ __launch_bounds__(256) void quant_block128_kernel(
 
 using namespace moe;
 
+// Rows of x (stride ldx) -> rows of q (stride ldq) with codes in [0, H) and
+// zero codes in [H, pad_to), scales [T, ceil(H/128)] with stride lds.
+static int quant_any(const void* x_bf16, int64_t ldx, int64_t T, int64_t H, int64_t pad_to, void* q_fp8,
+                     int64_t ldq, float* scales, int64_t lds, void* stream) {
+  const int64_t waves = T * ((pad_to + 127) / 128);
+  hipLaunchKernelGGL(quant_group128_any_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, ldx, T, H, pad_to, (uint8_t*)q_fp8, ldq, scales,
+                     lds);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 extern "C" int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void* q_fp8,
                                   float* scales, void* stream) {
   if (T < 0 || H < 0) return kErrBadShape;
   if (T == 0 || H == 0) return kOk;
   if (!x_bf16 || !q_fp8 || !scales) return kErrNullPointer;
-  if (H % 128 != 0) return kErrBadShape;
-  if (((uintptr_t)x_bf16 & 15) != 0 || ((uintptr_t)q_fp8 & 7) != 0) return kErrBadShape;
+  if ((H % 128 != 0 || ((uintptr_t)x_bf16 & 15) != 0 || ((uintptr_t)q_fp8 & 7) != 0)) {
+    if (((uintptr_t)x_bf16 & 1) != 0) return kErrBadShape;
+    if (T * ((H + 127) / 128) > (int64_t)0xFFFFFFFF * 4) return kErrBadShape;
+    return quant_any(x_bf16, H, T, H, H, q_fp8, H, scales, (H + 127) / 128, stream);
+  }
   const int64_t n_chunks = T * H / 8;
   constexpr int64_t per_block = kQuantThreads * quant_unroll<false>();
   const int64_t blocks = (n_chunks + per_block - 1) / per_block;
@@ -158,6 +203,19 @@ extern "C" int moe_quant_group128(const void* x_bf16, int64_t T, int64_t H, void
                      (hipStream_t)stream, (const uint16_t*)x_bf16, (uint8_t*)q_fp8, scales,
                      n_chunks, H / 8);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+extern "C" int moe_quant_group128_padded(const void* x_bf16, int64_t T, int64_t H, void* q_fp8, int64_t ldq,
+                                         float* scales, void* stream) {
+  if (T < 0 || H < 0) return kErrBadShape;
+  const int64_t hp = (H + 127) / 128 * 128;
+  if (ldq < hp) return kErrBadShape;
+  if (T == 0 || H == 0) return kOk;
+  if (!x_bf16 || !q_fp8 || !scales) return kErrNullPointer;
+  if (ldq == H) return moe_quant_group128(x_bf16, T, H, q_fp8, scales, stream);
+  if (((uintptr_t)x_bf16 & 1) != 0) return kErrBadShape;
+  if (T * (hp / 128) > (int64_t)0xFFFFFFFF * 4) return kErrBadShape;
+  return quant_any(x_bf16, H, T, H, hp, q_fp8, ldq, scales, hp / 128, stream);
 }
 
 extern "C" int moe_silu_mul_quant_group128(const void* c_bf16, int64_t R, int64_t I, void* q_fp8,

@@ -74,6 +74,23 @@ def _need_weights(w: torch.Tensor, w_scale: torch.Tensor, name: str) -> tuple[in
     return E, N, K
 
 
+def _pad_fp8(w: torch.Tensor, dim: int, size: int) -> torch.Tensor:
+    """FP8 weights [E, N, K] with dimension ``dim`` (1 or 2) zero-padded to
+    ``size``: the zero code, as the reference's 128x128 block quant pads a
+    ragged block (data/checkpoint.py:28-40), so the padded rows or columns
+    contribute nothing to a GEMM."""
+    if w.shape[dim] == size:
+        return w
+    shape = list(w.shape)
+    shape[dim] = size
+    out = torch.zeros(shape, dtype=torch.uint8, device=w.device)
+    if dim == 1:
+        out[:, : w.shape[1]] = w.view(torch.uint8)
+    else:
+        out[:, :, : w.shape[2]] = w.view(torch.uint8)
+    return out.view(FP8)
+
+
 def _need_routing(sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
                   num_tokens_post_padded: torch.Tensor, block_m: int) -> None:
     """moe_align_block_size outputs: one expert id per block of sorted positions."""
@@ -127,11 +144,12 @@ def _check_grouped_gemm(A, A_scale, B, B_scale, C, weights, sorted_token_ids, ex
 def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128,
                               out_q: torch.Tensor | None = None,
                               out_s: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """x [T,H] bf16 -> (q [T,H] e4m3fn, scales [T,H/128] fp32).
+    """x [T,H] bf16 -> (q [T,H] e4m3fn, scales [T,ceil(H/128)] fp32).
 
     Arithmetic of moe_bench/verify.py:108-117 (scale = max(amax/448, 1e-12),
-    q = e4m3(clamp(x/scale, +-448))); output form of vLLM's
-    per_token_group_quant_fp8 as consumed by the grouped GEMM."""
+    q = e4m3(clamp(x/scale, +-448)); a last group of H mod 128 columns is
+    quantised as the reference's zero padding leaves it); output form of
+    vLLM's per_token_group_quant_fp8 as consumed by the grouped GEMM."""
     if group_size != 128:
         raise NotImplementedError("only 1x128 activation groups are implemented")
     if x.dim() != 2:
@@ -139,9 +157,9 @@ def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128,
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
     q = torch.empty((T, H), dtype=FP8, device=x.device) if out_q is None else out_q
-    s = torch.empty((T, H // 128), dtype=torch.float32, device=x.device) if out_s is None else out_s
+    s = torch.empty((T, _blocks128(H)), dtype=torch.float32, device=x.device) if out_s is None else out_s
     _need(q, "out_q", FP8, (T, H))
-    _need(s, "out_s", torch.float32, (T, H // 128))
+    _need(s, "out_s", torch.float32, (T, _blocks128(H)))
     check(lib().moe_quant_group128(_ptr(x), T, H, _ptr(q), _ptr(s), _stream()), "moe_quant_group128")
     return q, s
 
@@ -581,6 +599,13 @@ class SharedExpertRunner:
     (shared_expert.py:3-7, 83-93).  Returns a [rows, H] bf16 view of an
     internal buffer (valid until the next call).
 
+    An H that is not a multiple of 128 runs at the padded width Hp =
+    ceil(H/128)*128: the weights get zero codes in the padding when the
+    runner is built, a bf16 ``x`` is quantised into zero-padded rows, and an
+    FP8 ``x`` must come in that padded layout ([rows, Hp], as
+    FusedExpertsRunner's own q1).  ``out`` then holds [max_tokens, Hp] rows
+    and the call returns their first H columns.
+
     Every buffer is allocated when the runner is built (the builder-allocates
     contract of schemes/base.py:45-93): the align outputs exist for
     ``max_tokens`` rows and for each count in ``row_counts``, or added later
@@ -596,19 +621,23 @@ class SharedExpertRunner:
             raise ValueError("the shared expert has exactly one expert")
         if w2.shape != (1, H, N2 // 2):
             raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w1 {tuple(w1.shape)}")
-        self.w1, self.w1_scale, self.w2, self.w2_scale = w1, w1_scale, w2, w2_scale
+        if (N2 // 2) % 128:
+            raise ValueError(f"the intermediate size {N2 // 2} must be a multiple of 128")
         self.H, self.I, self.max_tokens = H, N2 // 2, max_tokens
+        self.Hp = _blocks128(H) * 128
+        w1, w2 = _pad_fp8(w1, 2, self.Hp), _pad_fp8(w2, 1, self.Hp)
+        self.w1, self.w1_scale, self.w2, self.w2_scale = w1, w1_scale, w2, w2_scale
         self.BM = block_size_m or get_moe_config(max_tokens, 1, 1)["BLOCK_SIZE_M"]
         dev = w1.device
         self._aligns: dict[int, AlignBuffers] = {}
         for rows in (max_tokens, *row_counts):
             self.prepare(rows)
         mp = self._aligns[max_tokens].max_padded
-        self.q = torch.empty((max_tokens, H), dtype=FP8, device=dev)
-        self.s = torch.empty((max_tokens, H // 128), dtype=torch.float32, device=dev)
+        self.q = torch.empty((max_tokens, self.Hp), dtype=FP8, device=dev)
+        self.s = torch.empty((max_tokens, self.Hp // 128), dtype=torch.float32, device=dev)
         self.hq = torch.empty((mp, self.I), dtype=FP8, device=dev)
         self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
-        self.out = torch.empty((max_tokens, H), dtype=torch.bfloat16, device=dev)
+        self.out = torch.empty((max_tokens, self.Hp), dtype=torch.bfloat16, device=dev)
 
     def prepare(self, rows: int) -> None:
         """Build the align outputs for calls with ``rows`` tokens, all routed
@@ -638,22 +667,25 @@ class SharedExpertRunner:
                 raise ValueError(f"input_scale rows {input_scale.shape[0]} do not match input rows {rows}")
             q, s = x, input_scale
         else:
+            _need(x, "x", torch.bfloat16)
             if tuple(x.shape) != (rows, self.H):
                 raise ValueError(f"x must be [rows, {self.H}], got {tuple(x.shape)}")
-            q, s = per_token_group_quant_fp8(x, out_q=self.q[:rows], out_s=self.s[:rows])
-        _need(q, "x", FP8, (rows, self.H))
-        _need(s, "input_scale", torch.float32, (rows, self.H // 128))
+            q, s = self.q[:rows], self.s[:rows]
+            check(lib().moe_quant_group128_padded(_ptr(x), rows, self.H, _ptr(q), self.Hp, _ptr(s), _stream()),
+                  "moe_quant_group128_padded")
+        _need(q, "x", FP8, (rows, self.Hp))
+        _need(s, "input_scale", torch.float32, (rows, self.Hp // 128))
         a = self._align_for(rows)
         check(lib().moe_gemm_w13_silu_quant(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
                                             _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
-                                            self.H, self.I, 1, self.BM, a.max_padded, _ptr(self.hq),
+                                            self.Hp, self.I, 1, self.BM, a.max_padded, _ptr(self.hq),
                                             _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
         out = self.out[:rows]
         check(lib().moe_grouped_gemm(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
                                      _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), None, rows, 1, 1,
-                                     self.H, self.I, 1, self.BM, a.max_padded, _ptr(out), _stream()),
+                                     self.Hp, self.I, 1, self.BM, a.max_padded, _ptr(out), _stream()),
               "moe_grouped_gemm")
-        return out
+        return out[:, : self.H]
 
 
 class FusedExpertsRunner:
@@ -674,7 +706,18 @@ class FusedExpertsRunner:
     ``hs`` is then a [max_padded, I/128] view of the K-major buffer.  Run one
     stage at a time with ``stage_quant``, ``stage_align``, ``stage_scales``,
     ``stage_w13``, ``stage_w2``, ``stage_shared``, ``stage_reduce``, in that
-    order."""
+    order.
+
+    A hidden size H that is not a multiple of 128 runs at the padded width
+    Hp = ceil(H/128)*128, which is what the reference's quant does to the
+    activations (verify.py:111-113) and its weight quant to a ragged block
+    (data/checkpoint.py:28-40): the weights get zero codes in the padding
+    once, when the runner is built; the activations are quantised into
+    zero-padded rows; W2 writes Hp columns, and the top-k sum's first H
+    columns are the output.  The zero codes add nothing to any product, so
+    the results are those of the unpadded computation.  The intermediate
+    size I must be a multiple of 128 (the fused SiLU*up pairs whole gate and
+    up groups)."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
@@ -685,7 +728,11 @@ class FusedExpertsRunner:
         _need_weights(w2, w2_scale, "w2")
         if w2.shape != (E, H, N2 // 2):
             raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+        if (N2 // 2) % 128:
+            raise ValueError(f"the intermediate size {N2 // 2} must be a multiple of 128")
         self.E, self.H, self.I, self.T, self.top_k = E, H, N2 // 2, num_tokens, top_k
+        self.Hp = Hp = _blocks128(H) * 128
+        w13, w2 = _pad_fp8(w13, 2, Hp), _pad_fp8(w2, 1, Hp)
         self.S = num_tokens * top_k
         self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
         if self.BM not in SUPPORTED_BLOCK_M:
@@ -702,8 +749,8 @@ class FusedExpertsRunner:
         self.shared = shared
         self.shared_out: torch.Tensor | None = None
         dev = w13.device
-        self.q1 = torch.empty((self.T, H), dtype=FP8, device=dev)
-        self.s1 = torch.empty((self.T, H // 128), dtype=torch.float32, device=dev)
+        self.q1 = torch.empty((self.T, Hp), dtype=FP8, device=dev)
+        self.s1 = torch.empty((self.T, Hp // 128), dtype=torch.float32, device=dev)
         # Expert parallelism: align over the global experts, GEMMs over the
         # local ones (blocks of non-local experts are -1 and produce zeros).
         self.expert_map = None
@@ -722,24 +769,30 @@ class FusedExpertsRunner:
             scales_by_position = gemm_tile_rows(self.BM, self.S, self.E, self.tile_m) >= 128
         self.scales_by_position = bool(scales_by_position)
         if self.scales_by_position:
-            self.s1_pos = torch.empty((H // 128, mp), dtype=torch.float32, device=dev)
+            self.s1_pos = torch.empty((Hp // 128, mp), dtype=torch.float32, device=dev)
             self.hs_pos = torch.empty((self.I // 128, mp), dtype=torch.float32, device=dev)
             self.hs = self.hs_pos.t()  # [mp, I/128] view by position
         else:
             self.hs = torch.empty((mp, self.I // 128), dtype=torch.float32, device=dev)
-        self.D = torch.empty((max(self.S, 1), H), dtype=torch.bfloat16, device=dev)
+        self.D = torch.empty((max(self.S, 1), Hp), dtype=torch.bfloat16, device=dev)
         if out is not None:
             _need(out, "out", torch.bfloat16)
             if tuple(out.shape) != (self.T, H):
                 raise ValueError(f"out must be [{self.T}, {H}]")
         self.y = out if out is not None else torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
+        # the top-k sum at the padded width, whose first H columns are y
+        self.y_pad = self.y if Hp == H else torch.empty((self.T, Hp), dtype=torch.bfloat16, device=dev)
 
     def stage_quant(self, hidden: torch.Tensor) -> None:
         _need(hidden, "hidden_states", torch.bfloat16)
         if tuple(hidden.shape) != (self.T, self.H):
             raise ValueError(f"hidden_states must be [{self.T}, {self.H}]")
-        check(lib().moe_quant_group128(_ptr(hidden), self.T, self.H, _ptr(self.q1), _ptr(self.s1),
-                                       _stream()), "moe_quant_group128")
+        if self.Hp == self.H:
+            check(lib().moe_quant_group128(_ptr(hidden), self.T, self.H, _ptr(self.q1), _ptr(self.s1),
+                                           _stream()), "moe_quant_group128")
+        else:
+            check(lib().moe_quant_group128_padded(_ptr(hidden), self.T, self.H, _ptr(self.q1), self.Hp,
+                                                  _ptr(self.s1), _stream()), "moe_quant_group128_padded")
 
     def stage_align(self, topk_ids: torch.Tensor) -> None:
         self.align.run(topk_ids, self.expert_map)
@@ -749,7 +802,7 @@ class FusedExpertsRunner:
         (nothing to do on the row-major path)."""
         if self.scales_by_position:
             a = self.align
-            check(lib().moe_gather_scales_by_position(_ptr(self.s1), self.T, self.H // 128, _ptr(a.sorted_ids),
+            check(lib().moe_gather_scales_by_position(_ptr(self.s1), self.T, self.Hp // 128, _ptr(a.sorted_ids),
                                                       _ptr(a.ntpp), self.S, self.top_k, a.max_padded,
                                                       _ptr(self.s1_pos), _stream()), "moe_gather_scales_by_position")
 
@@ -758,13 +811,13 @@ class FusedExpertsRunner:
         if self.scales_by_position:
             check(lib().moe_gemm_w13_silu_quant_pos(_ptr(self.q1), _ptr(self.s1_pos), _ptr(self.w13),
                                                     _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
-                                                    _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
+                                                    _ptr(a.ntpp), self.S, self.top_k, self.Hp, self.I, self.E,
                                                     self.BM, a.max_padded, self.tile_m, _ptr(self.hq),
                                                     _ptr(self.hs_pos), _stream()), "moe_gemm_w13_silu_quant_pos")
             return
         check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(self.q1), _ptr(self.s1), _ptr(self.w13),
                                                   _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),
-                                                  _ptr(a.ntpp), self.S, self.top_k, self.H, self.I, self.E,
+                                                  _ptr(a.ntpp), self.S, self.top_k, self.Hp, self.I, self.E,
                                                   self.BM, a.max_padded, self.tile_m, _ptr(self.hq),
                                                   _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
 
@@ -776,13 +829,13 @@ class FusedExpertsRunner:
         if self.scales_by_position:
             check(lib().moe_grouped_gemm_pos(_ptr(self.hq), _ptr(self.hs_pos), _ptr(self.w2), _ptr(self.w2_scale),
                                              _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
-                                             _ptr(topk_weights), self.S, self.H, self.I, self.E, self.BM,
+                                             _ptr(topk_weights), self.S, self.Hp, self.I, self.E, self.BM,
                                              a.max_padded, self.tile_m, _ptr(self.D), _stream()),
                   "moe_grouped_gemm_pos")
             return
         check(lib().moe_grouped_gemm_tiled(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
                                            _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp),
-                                           _ptr(topk_weights), self.S, 1, 1, self.H, self.I, self.E, self.BM,
+                                           _ptr(topk_weights), self.S, 1, 1, self.Hp, self.I, self.E, self.BM,
                                            a.max_padded, 0, self.tile_m, _ptr(self.D), _stream()),
               "moe_grouped_gemm")
 
@@ -792,8 +845,12 @@ class FusedExpertsRunner:
             self.shared_out = self.shared(self.q1, self.s1)
 
     def stage_reduce(self) -> None:
-        moe_sum(self.D[: self.S], self.y, self.top_k,
-                addend=self.shared_out if self.shared is not None else None)
+        addend = None
+        if self.shared is not None:  # the shared expert's rows at the padded width
+            addend = self.shared.out[: self.T] if self.Hp != self.H else self.shared_out
+        moe_sum(self.D[: self.S], self.y_pad, self.top_k, addend=addend)
+        if self.y_pad is not self.y:
+            self.y.copy_(self.y_pad[:, : self.H])
 
     def run(self, hidden: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
         self.stage_quant(hidden)
@@ -927,6 +984,9 @@ class SplitExpertsRunner:
         self.BM = block_size_m or get_moe_config(num_tokens, E, top_k)["BLOCK_SIZE_M"]
         if self.BM not in SUPPORTED_BLOCK_M:
             raise ValueError(f"block_size_m must be one of {SUPPORTED_BLOCK_M}")
+        if H % 128 or self.I % 128:
+            raise ValueError("the K/N-split runner cuts H into whole 128-column blocks: H and the intermediate "
+                             "size must be multiples of 128 (FusedExpertsRunner pads other widths)")
         self.k_bounds = _split_bounds(H, n_chunks_gateup)
         self.n_bounds = _split_bounds(H, n_chunks_down)
         if shared is not None and (shared.H != H or shared.max_tokens < num_tokens):

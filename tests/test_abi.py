@@ -71,7 +71,11 @@ def test_validation_rejects_bad_arguments_without_device_work(L):
     assert L.moe_grouped_gemm(None, None, None, None, None, None, None, None, 10, 2, 0, 256, 256,
                               4, 64, 100, None, None) == E["MOE_ERR_NULL_POINTER"]
     # shapes that are not multiples of 128, bad block sizes, bad top-k, bad expert counts
-    assert L.moe_quant_group128(dummy, 4, 100, dummy, dummy, None) == E["MOE_ERR_BAD_SHAPE"]
+    odd = ctypes.c_void_p(ctypes.addressof(buf) + 1)  # a bf16 row start that is not 2-byte aligned
+    assert L.moe_quant_group128(odd, 4, 100, dummy, dummy, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_quant_group128_padded(dummy, 4, 100, dummy, 100, dummy, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_quant_group128_padded(odd, 4, 100, dummy, 128, dummy, None) == E["MOE_ERR_BAD_SHAPE"]
+    assert L.moe_quant_group128_padded(None, 4, 100, None, 128, None, None) == E["MOE_ERR_NULL_POINTER"]
     assert L.moe_quant_group128(None, -1, 128, None, None, None) == E["MOE_ERR_BAD_SHAPE"]
     assert L.moe_grouped_gemm(None, None, None, None, None, None, None, None, 10, 2, 0, 200, 256,
                               4, 64, 100, None, None) == E["MOE_ERR_BAD_SHAPE"]
