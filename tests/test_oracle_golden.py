@@ -9,6 +9,10 @@ uniformly scaled output fails with the scale reported).  The stage chain
 (quant -> align -> W13 -> silu*up -> quant -> W2 -> reduce) is held to the
 golden through the reference worker's gates (worker.py:107-146) and to an
 fp32 evaluation on its own dequantised intermediates through the 2e-2 bound.
+The two checkers the GPU layer tests use are pinned on their own:
+dequant_reference by a closed form (a scaled-permutation W2), and
+calibrated_atol by the torch restatement of the golden run in both of its
+activation modes (tests/calibrate_tolerance.py:17-25's rule).
 """
 from __future__ import annotations
 
@@ -117,3 +121,56 @@ def test_stage_chain_meets_golden_gates(routing):
     rep3 = oracle.compare_outputs(oracle.bf16_to_f32(bad["y"]), golden, atol=0.0, rtol=0.0,
                                   **oracle.DEFAULT_GATES)
     assert rep3["pass"] is False
+
+
+def test_dequant_reference_closed_form():
+    """dequant_reference on a W2 that is a scaled permutation: every expert's
+    dequantised W2 maps intermediate column perm[n] to output column n, so
+    y[t, n] = sum_i w[t,i] * s_w2(e) * deq(h[t*k+i, perm_e[n]]) exactly.  A
+    transposed weight, a dropped routed weight, a wrong scale axis or a slot
+    paired with the wrong expert moves whole entries."""
+    rng = np.random.default_rng(21)
+    T, k, H, I, E = 6, 2, 256, 256, 3
+    lut = oracle.e4m3_lut().astype(np.float64)
+    one = int(np.where(lut == 1.0)[0][0])
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k), dtype=np.float32) + np.float32(0.25)
+    hq = rng.integers(0, 0x7E, size=(T * k, I), dtype=np.uint8)
+    hs = (rng.random((T * k, I // 128)) + 0.5).astype(np.float32)
+    w2q = np.zeros((E, H, I), np.uint8)
+    perms = [rng.permutation(I)[:H] for _ in range(E)]
+    for e in range(E):
+        w2q[e, np.arange(H), perms[e]] = one
+    w2s = np.stack([np.full((H // 128, I // 128), 2.0 ** (e - 1), np.float32) for e in range(E)])
+    got = oracle.dequant_reference(hq, hs, ids, w, w2q, w2s).astype(np.float64)
+    h = lut[hq] * np.repeat(hs.astype(np.float64), 128, axis=1)
+    want = np.zeros((T, H))
+    for t in range(T):
+        for i in range(k):
+            e = ids[t, i]
+            want[t] += float(w[t, i]) * 2.0 ** (e - 1) * h[t * k + i, perms[e]]
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=0)
+
+
+def test_calibrated_atol_against_the_torch_golden():
+    """calibrated_atol is tests/calibrate_tolerance.py:17-25's rule, 1.5 x the
+    largest |golden(group128) - golden(no quant)|; held to the torch
+    restatement of the golden (oracle/golden_torch.py, pinned to the C oracle
+    separately) evaluated in both modes."""
+    import torch
+
+    from oracle.golden_torch import golden_moe_torch
+    c = make_case(T=40, H=256, I=256, E=4, k=2, BM=16, seed=13, routing="softmax")
+    w1 = dequant_weights_f32(c.w13_q, c.w13_s)
+    w2 = dequant_weights_f32(c.w2_q, c.w2_s)
+    x = oracle.bf16_to_f32(c.x)
+    args = (torch.from_numpy(np.asarray(x, np.float32)), torch.from_numpy(c.topk_ids).long(),
+            torch.from_numpy(c.topk_w), lambda e: torch.from_numpy(w1[e]), lambda e: torch.from_numpy(w2[e]))
+    fp8 = golden_moe_torch(*args, act_quant="group128").numpy()
+    none = golden_moe_torch(*args, act_quant="none").numpy()
+    want = 1.5 * float(np.abs(fp8 - none).max())
+    got = oracle.calibrated_atol(x, c.topk_ids, c.topk_w, w1, w2)
+    assert want > 0 and abs(got - want) <= 1e-5 * want + 1e-7, (got, want)
+    # a tolerance of another shape (the p99, or 1x the max) would differ
+    assert abs(got - 1.5 * float(np.quantile(np.abs(fp8 - none), 0.99))) > 1e-3 * want
+    assert abs(got - float(np.abs(fp8 - none).max())) > 0.3 * want
