@@ -35,6 +35,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "FP8 grouped-GEMM TFLOP/s (% MFMA peak) + MoE layer µs, DeepSeek-V3 shape, 1 GPU"
 PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 STAGES = ("quant", "align", "scales", "w13", "w2", "reduce")
 
@@ -150,6 +151,39 @@ def shared_expert_leg(runner, wl, steps: int, warmup: int) -> dict:
             "GB/s": bytes_ / sec / 1e9, "hbm_frac": bytes_ / sec / 1e9 / PEAK_HBM_GBS,
             "bound": "mfma" if flop / (PEAK_FP8_TFLOPS * 1e12) >= bytes_ / (PEAK_HBM_GBS * 1e9) else "hbm",
             "input": "the routed layer's FP8 activations and 1x128 scales (no second quant)"}
+
+
+def exact_dot_leg(runner, step, steps: int, warmup: int, flop_w13: float) -> dict:
+    """The layer with the W13 stage in exact-dot mode (every 128-element dot
+    as four bf16 MFMAs on the codes converted exactly to bf16): W13 and
+    layer time per call, timed with events like the headline layer.  The
+    headline numbers are the FP8 form; this is the cost of the opt-in mode."""
+    import torch
+    runner.exact_dot = True
+    try:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in ev:
+            a.record()
+            runner.stage_w13()
+            b.record()
+        lev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in lev:
+            a.record()
+            step()
+            b.record()
+        torch.cuda.synchronize()
+    finally:
+        runner.exact_dot = False
+    step()  # leave the runner's buffers as the FP8 form writes them
+    torch.cuda.synchronize()
+    w13 = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in ev])
+    tflops = flop_w13 / (w13["avg"] / 1e6) / 1e12
+    return {"w13_us_stats": w13, "layer_us_stats": summarize_samples([a.elapsed_time(b) * 1e3 for a, b in lev]),
+            "w13_TFLOP/s": tflops, "w13_bf16_mfma_frac": tflops / PEAK_BF16_TFLOPS,
+            "form": "FP8 codes converted to bf16, four v_mfma_f32_16x16x32_bf16 per 128-element dot"}
 
 
 def _amd_smi_sample() -> tuple[float, float] | None:
@@ -313,6 +347,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shared", action="store_true",
                     help="skip the shared-expert leg (one E=1, top-1 expert on the layer's FP8 input)")
+    ap.add_argument("--no-exact", action="store_true",
+                    help="skip the exact-dot leg (the layer with W13 in its exact-dot mode)")
     ap.add_argument("--power-seconds", type=float, default=2.0,
                     help="seconds of back-to-back layer, W13 and W2 runs sampled for socket power and clock "
                          "(0 to skip)")
@@ -511,6 +547,8 @@ def main() -> int:
                                      "sampled every ~0.2 s while the stage runs back to back"}
     if not args.no_shared:
         result["shared_expert"] = shared_expert_leg(runner, wl, args.steps, args.warmup)
+    if not args.no_exact:
+        result["exact_dot"] = exact_dot_leg(runner, step, args.steps, args.warmup, flop_w13)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(data, wl, args.cpu_budget)
         n_rows = min(wl.T, 1024) * wl.top_k

@@ -223,6 +223,24 @@ int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_pos, const 
                                 int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
                                 int64_t max_padded, int32_t tile_m, void* hq, float* hs_pos, void* stream);
 
+/* The fused W13 with exact dot products (an opt-in mode; its dots follow the
+ * reference's per-block product, overlap/kernels.py:172-179, without the FP8
+ * matrix core's truncation).  The FP8 16x16x128 instruction truncates the
+ * products of each group of 8 inside a 128-element dot, which moves about 1 %
+ * of the bf16 C13 values across a rounding boundary and about 0.2 % of the
+ * intermediate codes by up to a few ULPs.  This variant converts the FP8
+ * codes exactly to bf16 and takes every 128-element dot as four bf16 MFMAs,
+ * whose products are exact, at about twice the matrix-core time of the FP8
+ * form.  Same arguments and outputs as moe_gemm_w13_silu_quant_tiled with
+ * scales_by_position == 0, and as moe_gemm_w13_silu_quant_pos (A_scale and
+ * hs K-major by sorted position) with scales_by_position != 0. */
+int moe_gemm_w13_silu_quant_exact(const void* Aq, const float* A_scale, const void* W13,
+                                  const float* W13_scale, const int32_t* sorted_ids,
+                                  const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                  int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t block_size_m,
+                                  int64_t max_padded, int32_t tile_m, int32_t scales_by_position, void* hq,
+                                  float* hs, void* stream);
+
 /* The W2 GEMM (A rows by sorted position, as a_by_pos = 1, C rows by slot,
  * routed weights if topk_weights is not null) with A_scale_pos [K/128,
  * max_padded] K-major by sorted position, as moe_gemm_w13_silu_quant_pos

@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                                _i64, _i32, _i32, _i64, _P, _P, _P]),
     "moe_gemm_w13_silu_quant_tiled": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
                                                      _i64, _i32, _i32, _i64, _i32, _P, _P, _P]),
+    "moe_gemm_w13_silu_quant_exact": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _i64, _i32, _i64,
+                                                     _i64, _i32, _i32, _i64, _i32, _i32, _P, _P, _P]),
     "moe_silu_and_mul": (ctypes.c_int, [_P, _i64, _i64, _P, _P]),
     "moe_reduce_topk": (ctypes.c_int, [_P, _i64, _i32, _i64, _P, _P]),
 }

@@ -401,7 +401,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& g, v4f (&acc)[Tile
 // rows_avail) of the sorted order (a prefix of nvalid of them hold slots) of
 // expert e, with BM-row operand tiles.  A body with BM smaller than the tile
 // computes its first BM rows; the caller has checked that the rest are padding.
-template <int BM, bool FUSED>
+template <int BM, bool FUSED, bool EXACT = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
                                           int nvalid, bool b_nt) {
   using T = Tile<BM>;
@@ -594,23 +594,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         const uint8_t* pb0 = st + b_lane0;
         const uint8_t* pb1 = st + b_lane1;
         const float* tSA = smSA + stage * T::NS * 64 + sa_lane;
-        v8i af[RA];
-        [&]<int... R>(std::integer_sequence<int, R...>) {
-          ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
-        }(std::make_integer_sequence<int, RA>{});
-        // Weight fragments triple-buffered (two LDS reads in flight ahead of the
-        // MFMAs that use them); MFMA t is issued before the scale FMAs of MFMA
-        // t - kScaleLag, whose result is ready by then.  The MFMA takes the
-        // weight fragment first, so a lane's four results are four columns of
-        // one token: one scale product a_s * b_s per 16-row subtile and group.
-        constexpr int LG = kScaleLag;
-        constexpr int NQ = 2 * T::CS;  // weight fragments per step
-        constexpr int NT = NQ * RA;
-        constexpr int NBQ = 3;
-        v8i bq[NBQ];
-        v4f p[LG + 1];
+        // a_s * b_s of the step for each 16-row subtile and column group
         float sab[2][RA];
-        {
+        auto scale_products = [&] {
           const float sb0 = smSB[kk];
           const float sb1 = smSB[kMaxKB + kk];
 #pragma unroll
@@ -619,45 +605,96 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
             sab[0][r] = sa * sb0;
             sab[1][r] = sa * sb1;
           }
-        }
-        bq[0] = frag_at<0>(pb0, pb1);
-        if constexpr (NQ > 1) bq[1] = frag_at<(1 / T::CS * 128 + 1 % T::CS * 16) * 128>(pb0, pb1);
-        [&]<int... Q>(std::integer_sequence<int, Q...>) {
-          (
-              [&] {
-                if constexpr (Q + NBQ - 1 < NQ) {
-                  constexpr int gn = (Q + NBQ - 1) / T::CS, cn = (Q + NBQ - 1) % T::CS;
-                  bq[(Q + NBQ - 1) % NBQ] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
-                }
+        };
+        constexpr int NQ = 2 * T::CS;  // weight fragments per step
+        if constexpr (EXACT) {
+          // Exact dots on the bf16 matrix core: the step's A fragments are
+          // converted once, each weight fragment as it is read; every 128-K
+          // dot is four chained bf16 MFMAs, then scaled into acc as below.
+          scale_products();
+          v8bf abf[RA][4];
+          [&]<int... R>(std::integer_sequence<int, R...>) {
+            (
+                [&] {
+                  const v8i f = frag_at<R * 2048>(pa0, pa1);
 #pragma unroll
-                for (int r = 0; r < RA; ++r) {
-                  const int t = Q * RA + r;
-                  p[t % (LG + 1)] = mfma_fp8(bq[Q % NBQ], af[r]);
-                  if (t >= LG) {
-                    const int u = t - LG, uq = u / RA, ur = u % RA;
-                    const int ug = uq / T::CS, uc = uq % T::CS;
+                  for (int q = 0; q < 4; ++q) abf[R][q] = fp8_quarter_bf16(f, q);
+                }(),
+                ...);
+          }(std::make_integer_sequence<int, RA>{});
+          [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            (
+                [&] {
+                  constexpr int gq = Q / T::CS, cq = Q % T::CS;
+                  const v8i fb = frag_at<(gq * 128 + cq * 16) * 128>(pb0, pb1);
+                  v8bf bbf[4];
+#pragma unroll
+                  for (int q = 0; q < 4; ++q) bbf[q] = fp8_quarter_bf16(fb, q);
+#pragma unroll
+                  for (int r = 0; r < RA; ++r) {
+                    const v4f p = mfma_bf16_dot128(bbf, abf[r]);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                      acc[r][gq][cq][v] = __builtin_fmaf(p[v], sab[gq][r], acc[r][gq][cq][v]);
+                  }
+                }(),
+                ...);
+          }(std::make_integer_sequence<int, NQ>{});
+        } else {
+          v8i af[RA];
+          [&]<int... R>(std::integer_sequence<int, R...>) {
+            ((af[R] = frag_at<R * 2048>(pa0, pa1)), ...);
+          }(std::make_integer_sequence<int, RA>{});
+          // Weight fragments triple-buffered (two LDS reads in flight ahead of the
+          // MFMAs that use them); MFMA t is issued before the scale FMAs of MFMA
+          // t - kScaleLag, whose result is ready by then.  The MFMA takes the
+          // weight fragment first, so a lane's four results are four columns of
+          // one token: one scale product a_s * b_s per 16-row subtile and group.
+          constexpr int LG = kScaleLag;
+          constexpr int NT = NQ * RA;
+          constexpr int NBQ = 3;
+          v8i bq[NBQ];
+          v4f p[LG + 1];
+          scale_products();
+          bq[0] = frag_at<0>(pb0, pb1);
+          if constexpr (NQ > 1) bq[1] = frag_at<(1 / T::CS * 128 + 1 % T::CS * 16) * 128>(pb0, pb1);
+          [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            (
+                [&] {
+                  if constexpr (Q + NBQ - 1 < NQ) {
+                    constexpr int gn = (Q + NBQ - 1) / T::CS, cn = (Q + NBQ - 1) % T::CS;
+                    bq[(Q + NBQ - 1) % NBQ] = frag_at<(gn * 128 + cn * 16) * 128>(pb0, pb1);
+                  }
+#pragma unroll
+                  for (int r = 0; r < RA; ++r) {
+                    const int t = Q * RA + r;
+                    p[t % (LG + 1)] = mfma_fp8(bq[Q % NBQ], af[r]);
+                    if (t >= LG) {
+                      const int u = t - LG, uq = u / RA, ur = u % RA;
+                      const int ug = uq / T::CS, uc = uq % T::CS;
+#pragma unroll
+                      for (int v = 0; v < 4; ++v)
+                        acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sab[ug][ur], acc[ur][ug][uc][v]);
+                    }
+                  }
+                }(),
+                ...);
+          }(std::make_integer_sequence<int, NQ>{});
+          [&]<int... D>(std::integer_sequence<int, D...>) {  // drain the last LG MFMAs
+            (
+                [&] {
+                  constexpr int u = NT - LG + D;
+                  if constexpr (u >= 0) {
+                    constexpr int uq = u / RA, ur = u % RA;
+                    constexpr int ug = uq / T::CS, uc = uq % T::CS;
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
                       acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sab[ug][ur], acc[ur][ug][uc][v]);
                   }
-                }
-              }(),
-              ...);
-        }(std::make_integer_sequence<int, NQ>{});
-        [&]<int... D>(std::integer_sequence<int, D...>) {  // drain the last LG MFMAs
-          (
-              [&] {
-                constexpr int u = NT - LG + D;
-                if constexpr (u >= 0) {
-                  constexpr int uq = u / RA, ur = u % RA;
-                  constexpr int ug = uq / T::CS, uc = uq % T::CS;
-#pragma unroll
-                  for (int v = 0; v < 4; ++v)
-                    acc[ur][ug][uc][v] = __builtin_fmaf(p[u % (LG + 1)][v], sab[ug][ur], acc[ur][ug][uc][v]);
-                }
-              }(),
-              ...);
-        }(std::make_integer_sequence<int, LG>{});
+                }(),
+                ...);
+          }(std::make_integer_sequence<int, LG>{});
+        }
       }
       stage = (stage == T::KS - 1) ? 0 : stage + 1;
     }
@@ -679,11 +716,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
 // A tile of a BM-row launch whose valid rows fit SUB rows, run with the
 // SUB-row body.  Positions [SUB, rows_avail) are padding: the fused outputs
 // there are the zero codes and floor scales an all-zero row quantises to.
-template <int SUB, int BM, bool FUSED>
+template <int SUB, int BM, bool FUSED, bool EXACT>
 __device__ __forceinline__ void short_tile(const GemmArgs& g, int64_t j, int64_t pos0, int rows_avail, int e,
                                            int nvalid) {
   static_assert(Tile<SUB>::THREADS == Tile<BM>::THREADS, "same workgroup size");
-  gemm_tile<SUB, FUSED>(g, j, pos0, rows_avail, e, nvalid, false);
+  gemm_tile<SUB, FUSED, EXACT>(g, j, pos0, rows_avail, e, nvalid, false);
   if (FUSED) {
     const int tid = threadIdx.x;
     for (int ci = SUB * 8 + tid; ci < rows_avail * 8; ci += Tile<BM>::THREADS) {
@@ -700,11 +737,14 @@ constexpr int kernel_lds() {
   return BM == 256 && Tile<128>::LDS_BYTES > Tile<256>::LDS_BYTES ? Tile<128>::LDS_BYTES : Tile<BM>::LDS_BYTES;
 }
 
-template <int BM, bool FUSED>
-__global__ __launch_bounds__(Tile<BM>::THREADS)
-__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU, Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU)))
-void grouped_gemm_kernel(GemmArgs g) {
+// One workgroup of a BM-row launch: the tile map below, then the tile's body.
+// EXACT (fused W13 only) takes the dots on the bf16 matrix core; its 256-row
+// launch runs each tile as two 128-row bodies, since the bf16 fragments of the
+// 256-row body do not fit in the registers.
+template <int BM, bool FUSED, bool EXACT>
+__device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   using T = Tile<BM>;
+  static_assert(FUSED || !EXACT, "the exact-dot form is built for the fused W13 GEMM");
   static_assert(BM <= kTailRows || Tile<kTailRows>::LDS_BYTES <= kernel_lds<BM>(),
                 "the short body must fit in the launch's LDS");
   const int tid = threadIdx.x;
@@ -843,13 +883,22 @@ void grouped_gemm_kernel(GemmArgs g) {
   // subtiles instead of leaving half of the 256-row body's MFMAs on padding.
   if constexpr (BM > kTailRows) {
     if (nvalid <= kTailRows) {
-      short_tile<kTailRows, BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+      short_tile<kTailRows, BM, FUSED, EXACT>(g, j, pos0, rows_avail, e, nvalid);
       return;
     }
   }
   if constexpr (BM == 256) {
     if (nvalid <= 128) {
-      short_tile<128, BM, FUSED>(g, j, pos0, rows_avail, e, nvalid);
+      short_tile<128, BM, FUSED, EXACT>(g, j, pos0, rows_avail, e, nvalid);
+      return;
+    }
+    if constexpr (EXACT) {
+      // rows [0, 128) and then [128, rows_avail), whose valid rows are
+      // [128, nvalid); the barrier keeps the second body's first loads out of
+      // the LDS the first one's copy-out still reads
+      gemm_tile<128, FUSED, EXACT>(g, j, pos0, 128, e, 128, false);
+      __syncthreads();
+      gemm_tile<128, FUSED, EXACT>(g, j, pos0 + 128, rows_avail - 128, e, nvalid - 128, false);
       return;
     }
   }
@@ -857,33 +906,52 @@ void grouped_gemm_kernel(GemmArgs g) {
   // the only readers of their weight tiles: those loads carry the
   // non-temporal hint.  Experts with several row tiles, and taller tiles,
   // share weight tiles through L2 and load them cached.
-  gemm_tile<BM, FUSED>(g, j, pos0, rows_avail, e, nvalid, BM <= 32 && units == 1);
+  if constexpr (!(EXACT && BM == 256)) gemm_tile<BM, FUSED, EXACT>(g, j, pos0, rows_avail, e, nvalid, BM <= 32 && units == 1);
 }
 
 template <int BM, bool FUSED>
+__global__ __launch_bounds__(Tile<BM>::THREADS)
+__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU, Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU)))
+void grouped_gemm_kernel(GemmArgs g) {
+  grouped_gemm_body<BM, FUSED, false>(g);
+}
+
+// The fused W13 GEMM with exact dots (moe_gemm_w13_silu_quant_exact).
+template <int BM>
+__global__ __launch_bounds__(Tile<BM>::THREADS)
+__attribute__((amdgpu_waves_per_eu(Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU, Tile<BM>::NW / 4 * Tile<BM>::WG_PER_CU)))
+void w13_exact_kernel(GemmArgs g) {
+  grouped_gemm_body<BM, true, true>(g);
+}
+
+template <int BM, bool FUSED, bool EXACT>
 static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   using T = Tile<BM>;
+  const void* fn = EXACT ? (const void*)w13_exact_kernel<BM> : (const void*)grouped_gemm_kernel<BM, FUSED>;
   // Set once per process (a function-local static is initialised exactly once,
   // also when several host threads make their first call together).
-  static const hipError_t attr_rc = hipFuncSetAttribute(
-      (const void*)grouped_gemm_kernel<BM, FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, kernel_lds<BM>());
+  static const hipError_t attr_rc =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kernel_lds<BM>());
   if (attr_rc != hipSuccess) return kErrLaunch;
   // Upper bound on the tile count (the real one depends on ntpp, on the device).
   const int64_t grid = (args.max_blocks * args.n_tiles + kXcds - 1) / kXcds * kXcds;
   if (grid <= 0) return kOk;
-  hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(T::THREADS),
-                     kernel_lds<BM>(), st, args);
+  if constexpr (EXACT)
+    hipLaunchKernelGGL((w13_exact_kernel<BM>), dim3((unsigned)grid), dim3(T::THREADS), kernel_lds<BM>(), st, args);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM, FUSED>), dim3((unsigned)grid), dim3(T::THREADS), kernel_lds<BM>(),
+                       st, args);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-template <bool FUSED>
+template <bool FUSED, bool EXACT = false>
 static int dispatch_gemm(int TM, const GemmArgs& args, hipStream_t st) {
   switch (TM) {
-    case 16: return launch_gemm<16, FUSED>(args, st);
-    case 32: return launch_gemm<32, FUSED>(args, st);
-    case 64: return launch_gemm<64, FUSED>(args, st);
-    case 128: return launch_gemm<128, FUSED>(args, st);
-    case 256: return launch_gemm<256, FUSED>(args, st);
+    case 16: return launch_gemm<16, FUSED, EXACT>(args, st);
+    case 32: return launch_gemm<32, FUSED, EXACT>(args, st);
+    case 64: return launch_gemm<64, FUSED, EXACT>(args, st);
+    case 128: return launch_gemm<128, FUSED, EXACT>(args, st);
+    case 256: return launch_gemm<256, FUSED, EXACT>(args, st);
     default: return kErrBadBlockSize;
   }
 }
@@ -1105,11 +1173,12 @@ extern "C" int moe_grouped_gemm_k_split(const void* A, const float* A_scale, int
 }
 
 // The fused W13 GEMM; scales row-major (A_scale by token, hs by position), or
-// both K-major by sorted position when scales_by_pos.
+// both K-major by sorted position when scales_by_pos; exact dots on the bf16
+// matrix core when exact.
 static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const float* W13_scale,
                     const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
                     int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM, int64_t max_padded,
-                    int32_t tile_m, bool scales_by_pos, void* hq, float* hs, void* stream) {
+                    int32_t tile_m, bool scales_by_pos, bool exact, void* hq, float* hs, void* stream) {
   if (S < 0 || H <= 0 || I <= 0 || max_padded < 0) return kErrBadShape;
   if (H % 128 != 0 || I % 128 != 0 || H > 128 * kMaxKB) return kErrBadShape;
   if (top_k <= 0) return kErrBadTopK;
@@ -1145,7 +1214,7 @@ static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const
   g.E = E;
   dense_strides(g);
   if (scales_by_pos) g.as_pos_ld = g.hs_pos_ld = max_padded;
-  return dispatch_gemm<true>(TM, g, (hipStream_t)stream);
+  return exact ? dispatch_gemm<true, true>(TM, g, (hipStream_t)stream) : dispatch_gemm<true>(TM, g, (hipStream_t)stream);
 }
 
 extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scale, const void* W13,
@@ -1155,7 +1224,7 @@ extern "C" int moe_gemm_w13_silu_quant_tiled(const void* Aq, const float* A_scal
                                              int64_t max_padded, int32_t tile_m, void* hq, float* hs,
                                              void* stream) {
   return w13_gemm(Aq, A_scale, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k, H, I, E, BM, max_padded,
-                  tile_m, false, hq, hs, stream);
+                  tile_m, false, false, hq, hs, stream);
 }
 
 extern "C" int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_pos, const void* W13,
@@ -1165,7 +1234,17 @@ extern "C" int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_
                                            int64_t max_padded, int32_t tile_m, void* hq, float* hs_pos,
                                            void* stream) {
   return w13_gemm(Aq, A_scale_pos, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k, H, I, E, BM, max_padded,
-                  tile_m, true, hq, hs_pos, stream);
+                  tile_m, true, false, hq, hs_pos, stream);
+}
+
+extern "C" int moe_gemm_w13_silu_quant_exact(const void* Aq, const float* A_scale, const void* W13,
+                                             const float* W13_scale, const int32_t* sorted_ids,
+                                             const int32_t* expert_ids, const int32_t* ntpp, int64_t S,
+                                             int32_t top_k, int64_t H, int64_t I, int32_t E, int32_t BM,
+                                             int64_t max_padded, int32_t tile_m, int32_t scales_by_position,
+                                             void* hq, float* hs, void* stream) {
+  return w13_gemm(Aq, A_scale, W13, W13_scale, sorted_ids, expert_ids, ntpp, S, top_k, H, I, E, BM, max_padded,
+                  tile_m, scales_by_position != 0, true, hq, hs, stream);
 }
 
 namespace moe {

@@ -384,10 +384,14 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
                         w13_scale: torch.Tensor, sorted_token_ids: torch.Tensor,
                         expert_ids: torch.Tensor, num_tokens_post_padded: torch.Tensor,
                         num_slots: int, top_k: int, block_size_m: int,
-                        hq: torch.Tensor | None = None, hs: torch.Tensor | None = None, tile_m: int = 0):
+                        hq: torch.Tensor | None = None, hs: torch.Tensor | None = None, tile_m: int = 0,
+                        exact_dot: bool = False):
     """W13 GEMM + SiLU*up + 1x128 quant of h, outputs by sorted position:
     (hq [max_padded, I] e4m3fn, hs [max_padded, I/128] fp32).  ``tile_m`` as
-    for dispatch_fused_moe_kernel."""
+    for dispatch_fused_moe_kernel.  ``exact_dot`` takes every 128-element dot
+    exactly (the FP8 codes on the bf16 matrix core, about twice the
+    matrix-core time) instead of with the FP8 instruction's in-group product
+    truncation."""
     E, N2, H = _need_weights(w13, w13_scale, "w13")
     I = N2 // 2
     _need_routing(sorted_token_ids, expert_ids, num_tokens_post_padded, block_size_m)
@@ -401,6 +405,14 @@ def gemm_w13_silu_quant(Aq: torch.Tensor, A_scale: torch.Tensor, w13: torch.Tens
         hs = torch.empty((max_padded, I // 128), dtype=torch.float32, device=Aq.device)
     _need(hq, "hq", FP8, (max_padded, I))
     _need(hs, "hs", torch.float32, (max_padded, _blocks128(I)))
+    if exact_dot:
+        check(lib().moe_gemm_w13_silu_quant_exact(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
+                                                  _ptr(sorted_token_ids), _ptr(expert_ids),
+                                                  _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
+                                                  block_size_m, max_padded, int(tile_m), 0, _ptr(hq), _ptr(hs),
+                                                  _stream()),
+              "moe_gemm_w13_silu_quant_exact")
+        return hq, hs
     check(lib().moe_gemm_w13_silu_quant_tiled(_ptr(Aq), _ptr(A_scale), _ptr(w13), _ptr(w13_scale),
                                               _ptr(sorted_token_ids), _ptr(expert_ids),
                                               _ptr(num_tokens_post_padded), num_slots, top_k, H, I, E,
@@ -717,13 +729,20 @@ class FusedExpertsRunner:
     columns are the output.  The zero codes add nothing to any product, so
     the results are those of the unpadded computation.  The intermediate
     size I must be a multiple of 128 (the fused SiLU*up pairs whole gate and
-    up groups)."""
+    up groups).
+
+    ``exact_dot`` (also settable on the runner between runs) makes the W13
+    stage take every 128-element dot exactly: the FP8 codes converted to bf16
+    on the bf16 matrix core, about twice the matrix-core time of the FP8
+    instruction, whose in-group product truncation otherwise moves about
+    0.2 % of the intermediate codes.  W2 and every other stage are the same
+    in both modes."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
                  shared: SharedExpertRunner | None = None, out: torch.Tensor | None = None,
                  global_num_experts: int | None = None, expert_map: torch.Tensor | None = None,
-                 tile_m: int = 0, scales_by_position: bool | None = None):
+                 tile_m: int = 0, scales_by_position: bool | None = None, exact_dot: bool = False):
         E, N2, H = _need_weights(w13, w13_scale, "w13")
         _need_weights(w2, w2_scale, "w2")
         if w2.shape != (E, H, N2 // 2):
@@ -731,6 +750,7 @@ class FusedExpertsRunner:
         if (N2 // 2) % 128:
             raise ValueError(f"the intermediate size {N2 // 2} must be a multiple of 128")
         self.E, self.H, self.I, self.T, self.top_k = E, H, N2 // 2, num_tokens, top_k
+        self.exact_dot = bool(exact_dot)
         self.Hp = Hp = _blocks128(H) * 128
         w13, w2 = _pad_fp8(w13, 2, Hp), _pad_fp8(w2, 1, Hp)
         self.S = num_tokens * top_k
@@ -808,6 +828,16 @@ class FusedExpertsRunner:
 
     def stage_w13(self) -> None:
         a = self.align
+        if self.exact_dot:
+            by_pos = self.scales_by_position
+            check(lib().moe_gemm_w13_silu_quant_exact(_ptr(self.q1), _ptr(self.s1_pos if by_pos else self.s1),
+                                                      _ptr(self.w13), _ptr(self.w13_scale), _ptr(a.sorted_ids),
+                                                      _ptr(a.expert_ids), _ptr(a.ntpp), self.S, self.top_k,
+                                                      self.Hp, self.I, self.E, self.BM, a.max_padded, self.tile_m,
+                                                      int(by_pos), _ptr(self.hq),
+                                                      _ptr(self.hs_pos if by_pos else self.hs), _stream()),
+                  "moe_gemm_w13_silu_quant_exact")
+            return
         if self.scales_by_position:
             check(lib().moe_gemm_w13_silu_quant_pos(_ptr(self.q1), _ptr(self.s1_pos), _ptr(self.w13),
                                                     _ptr(self.w13_scale), _ptr(a.sorted_ids), _ptr(a.expert_ids),

@@ -109,6 +109,8 @@ SPEC = SchemeSpec(
         "n_streams": TunableSpec(int, 1, "HIP streams for the chunk pipeline (default priority)"),
         "n_chunks_gateup": TunableSpec(int, 0, "K chunks of W13 (the b schemes' structure); 0 = one pass"),
         "n_chunks_down": TunableSpec(int, 0, "N chunks of W2 (the b schemes' structure); 0 = one pass"),
+        "exact_dot": TunableSpec(bool, False, "W13 dots exact on the bf16 matrix core (no FP8 in-group "
+                                              "truncation; about twice the W13 matrix-core time)"),
     },
 )
 
@@ -134,6 +136,9 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
     if kn[0] > 0 and tunables["n_chunks"] > 1:
         raise SchemeConfigError(f"{SPEC.code}: n_chunks_gateup/n_chunks_down (K/N chunks) and n_chunks "
                                 "(token chunks) do not combine")
+    if kn[0] > 0 and tunables["exact_dot"]:
+        raise SchemeConfigError(f"{SPEC.code}: exact_dot is a mode of the fused W13; the K-split W13 "
+                                "(n_chunks_gateup) does not fuse")
 
     ckpt = data.ckpt
     w1, w1s = ckpt.w1.fp8.contiguous(), ckpt.w1.scale.float().contiguous()
@@ -159,10 +164,13 @@ def build(cfg: Any, ctx: Any, data: Any, scheme_cfg: Any) -> SchemeInstance:
     elif tunables["n_chunks"] > 1:
         runner = ops.ChunkedExpertsRunner(w1, w1s, w2, w2s, T, k, tunables["n_chunks"], tunables["n_streams"],
                                           block_m, shared_weights=shared_w)
+        for r in runner.runners:
+            r.exact_dot = tunables["exact_dot"]
         first = runner.runners[0]
     else:
         shared = ops.SharedExpertRunner(*shared_w, max_tokens=T) if shared_w is not None else None
-        runner = ops.FusedExpertsRunner(w1, w1s, w2, w2s, T, k, block_m, shared=shared)
+        runner = ops.FusedExpertsRunner(w1, w1s, w2, w2s, T, k, block_m, shared=shared,
+                                        exact_dot=tunables["exact_dot"])
         first = runner
 
     state: dict[str, Any] = {"runner": runner}

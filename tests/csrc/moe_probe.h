@@ -17,7 +17,8 @@
  *      quarter of K non-zero, summed by fp32 adds
  *   4  the codes converted to bf16 (exactly) and four
  *      v_mfma_f32_16x16x32_bf16, the accumulator chained through the
- *      instruction
+ *      instruction: the exact-dot form of moe_gemm_w13_silu_quant_exact,
+ *      through the same code
  */
 #ifndef MOE_PROBE_H
 #define MOE_PROBE_H
@@ -46,6 +47,10 @@ int moe_probe_block_gemm(const void* A, const float* As, const void* B, const fl
  * iterations of 8 independent 128-element dots on register operands and
  * write one checksum per lane to sink [waves * 64] (so nothing is elided). */
 int moe_probe_mfma_rate(int64_t waves, int32_t iters, int32_t form, float* sink, void* stream);
+
+/* The exact-dot form's FP8 -> bf16 converter: n e4m3fn codes (n a multiple
+ * of 8, 8-byte aligned) -> n bf16 bit patterns. */
+int moe_probe_fp8_to_bf16(const void* codes, int64_t n, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,32 +24,17 @@ __device__ __forceinline__ v8i only_quarter(const v8i& f, int q) {
   return r;
 }
 
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
-// The 8 FP8 codes of quarter q as bf16 (exact: every e4m3 value is a bf16).
-__device__ __forceinline__ v8bf quarter_bf16(const v8i& f, int q) {
-  const int lo = f[2 * q], hi = f[2 * q + 1];
-  v8bf r;
-  r[0] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 0);
-  r[1] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 1);
-  r[2] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 2);
-  r[3] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(lo, 3);
-  r[4] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 0);
-  r[5] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 1);
-  r[6] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 2);
-  r[7] = (__bf16)__builtin_amdgcn_cvt_f32_fp8(hi, 3);
-  return r;
-}
-
 __device__ __forceinline__ v4f dot_form(const v8i& a, const v8i& b, int form) {
   const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
   if (form == 0) return mfma_fp8(a, b);
-  if (form == 4) {
-    v4f acc = zero;
+  if (form == 4) {  // the exact-dot form of the grouped GEMM (mfma_frag.hpp)
+    v8bf aq[4], bq[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(quarter_bf16(a, q), quarter_bf16(b, q), acc, 0, 0, 0);
-    return acc;
+    for (int q = 0; q < 4; ++q) {
+      aq[q] = fp8_quarter_bf16(a, q);
+      bq[q] = fp8_quarter_bf16(b, q);
+    }
+    return mfma_bf16_dot128(aq, bq);
   }
   v4f acc = zero;
 #pragma unroll
@@ -152,9 +137,36 @@ __global__ __launch_bounds__(256) void rate_kernel(int iters, int form, float* _
   sink[gl] = s;
 }
 
+// Each thread converts 8 codes (two dwords, quarter 0 of a fragment) with
+// the exact-dot form's converter and writes their bf16 bits.
+__global__ __launch_bounds__(256) void fp8_bf16_kernel(const uint32_t* __restrict__ codes, int64_t n8,
+                                                        uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  v8i f = {0, 0, 0, 0, 0, 0, 0, 0};
+  f[0] = (int)codes[2 * i];
+  f[1] = (int)codes[2 * i + 1];
+  const v4u w = __builtin_bit_cast(v4u, fp8_quarter_bf16(f, 0));  // whole-vector cast (see mfma_frag.hpp)
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    out[8 * i + 2 * c] = (uint16_t)(w[c] & 0xFFFFu);
+    out[8 * i + 2 * c + 1] = (uint16_t)(w[c] >> 16);
+  }
+}
+
 }  // namespace moe_probe
 
 using namespace moe_probe;
+
+extern "C" int moe_probe_fp8_to_bf16(const void* codes, int64_t n, void* out, void* stream) {
+  if (!codes || !out) return kErrNullPointer;
+  if (n <= 0 || n % 8 || n > ((int64_t)1 << 30) || ((uintptr_t)codes & 7) || ((uintptr_t)out & 1))
+    return kErrBadShape;
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(fp8_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint32_t*)codes, n8, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
 
 extern "C" int moe_probe_mfma_dot(const void* A, const void* B, float* C, int64_t n, int32_t form, void* stream) {
   if (!A || !B || !C) return kErrNullPointer;

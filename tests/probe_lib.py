@@ -18,6 +18,7 @@ SIGNATURES = {
     "moe_probe_mfma_dot": (ctypes.c_int, [_P, _P, _P, _i64, _i32, _P]),
     "moe_probe_block_gemm": (ctypes.c_int, [_P, _P, _P, _P, _i64, _i64, _i64, _i32, _P, _P]),
     "moe_probe_mfma_rate": (ctypes.c_int, [_i64, _i32, _i32, _P, _P]),
+    "moe_probe_fp8_to_bf16": (ctypes.c_int, [_P, _i64, _P, _P]),
 }
 
 # dot forms of moe_probe.h

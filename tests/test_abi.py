@@ -85,6 +85,12 @@ def test_validation_rejects_bad_arguments_without_device_work(L):
                               4, 64, 100, None, None) == E["MOE_ERR_BAD_TOPK"]
     assert L.moe_gemm_w13_silu_quant(None, None, None, None, None, None, None, 10, 2, 256, 256,
                                      0, 64, 100, None, None, None) == E["MOE_ERR_BAD_EXPERTS"]
+    assert L.moe_gemm_w13_silu_quant_exact(None, None, None, None, None, None, None, 10, 2, 256, 256, 4, 64, 100,
+                                           0, 1, None, None, None) == E["MOE_ERR_NULL_POINTER"]
+    assert L.moe_gemm_w13_silu_quant_exact(None, None, None, None, None, None, None, 10, 2, 256, 256, 4, 48, 100,
+                                           0, 0, None, None, None) == E["MOE_ERR_BAD_BLOCK_SIZE"]
+    assert L.moe_gemm_w13_silu_quant_exact(None, None, None, None, None, None, None, 10, 2, 200, 256, 4, 64, 100,
+                                           0, 0, None, None, None) == E["MOE_ERR_BAD_SHAPE"]
     assert L.moe_align_block_size(None, 10, 4, 16, None, None, None, 100, None, None) == \
         E["MOE_ERR_NULL_POINTER"]
     assert L.moe_align_block_size(dummy, 10, 4, 16, dummy, dummy, dummy, 10, dummy, None) == \

@@ -29,7 +29,7 @@ import numpy as np
 import pytest
 
 import oracle
-from moe_cases import a7_account, a7_assert, bf16_bits, u8_bits
+from moe_cases import A7_MAX_FRAC, A7_MAX_ULP, a7_account, a7_assert, bf16_bits, e4m3_ulp_diff, u8_bits
 from tile_map import COL_MAJOR_K, pick_tiles, tile_map, tile_positions
 
 pytestmark = pytest.mark.gpu
@@ -83,6 +83,27 @@ def _only(host, ti, BM):
     return srt, eids
 
 
+def _fused_ref(layer, name, ti):
+    """The oracle chain of a picked tile's fused outputs (C13 of gate group j
+    and up group I/128 + j by slot, with its fp32 value and bound, then h, the
+    codes and the scale), computed once per layer and tile."""
+    wl, d, runner, C13, h, host, tile_m = layer
+    cache = host.setdefault("fused_ref", {})
+    if name not in cache:
+        S, I, BM = wl.S, wl.I, wl.block_m
+        pos = tile_positions(ti, host["sorted"], S)
+        slots = host["sorted"][pos]
+        srt, eids = _only(host, ti, BM)
+        B, Bs = _expert_cols(d.w13, d.w13_s, ti.expert, [ti.j, I // 128 + ti.j])
+        cref, cf32, cbnd = oracle.grouped_gemm(host["q1"], host["s1"], B, Bs, srt, eids, host["ntpp"], BM, S,
+                                               wl.top_k, with_f32=True, with_bound=True)
+        cref, cf32, cbnd = cref[slots], cf32[slots], cbnd[slots]
+        href = oracle.silu_and_mul(cref)
+        qref, sref = oracle.quant_group128(href)
+        cache[name] = (cref, cf32, cbnd, href, qref, sref)
+    return cache[name]
+
+
 def test_w13_whole_tiles(layer):
     wl, d, runner, C13, h, host, tile_m = layer
     S, I, BM = wl.S, wl.I, wl.block_m
@@ -104,13 +125,7 @@ def test_w13_whole_tiles(layer):
         print(f"  W13 {name}: {ti} rows {pos.size}, outside bound {int(bad.sum())}", flush=True)
         assert not bad.any(), f"W13 tile {name}: {int(bad.sum())} of {bad.size} outside the bound"
         # fused codes of group j: gate group j and up group I/128 + j
-        fgroups = [ti.j, I // 128 + ti.j]
-        B, Bs = _expert_cols(d.w13, d.w13_s, ti.expert, fgroups)
-        cref, cf32, cbnd = oracle.grouped_gemm(host["q1"], host["s1"], B, Bs, srt, eids, host["ntpp"], BM, S,
-                                               wl.top_k, with_f32=True, with_bound=True)
-        cref, cf32, cbnd = cref[slots], cf32[slots], cbnd[slots]
-        href = oracle.silu_and_mul(cref)
-        qref, sref = oracle.quant_group128(href)
+        cref, cf32, cbnd, href, qref, sref = _fused_ref(layer, name, ti)
         cols = np.r_[128 * ti.j:128 * ti.j + 128]
         c_gpu = np.concatenate([c13[slots][:, cols], c13[slots][:, I + cols]], axis=1)
         rep = a7_account(host["hq"][pos][:, cols], host["hs"][pos][:, ti.j:ti.j + 1], h_gpu[slots][:, cols], c_gpu,
@@ -137,3 +152,38 @@ def test_w2_whole_tiles(layer):
         bad = oracle.gemm_close(got, ref[slots], bnd[slots])
         print(f"  W2 {name}: {ti} rows {pos.size}, outside bound {int(bad.sum())}", flush=True)
         assert not bad.any(), f"W2 tile {name}: {int(bad.sum())} of {bad.size} outside the bound"
+
+
+def test_w13_exact_whole_tiles(layer):
+    """The exact-dot W13 on the same full-size layer: every picked tile's codes
+    within the north-star bar (<= 1 ULP on <= 0.1 % of codes) of the oracle
+    chain, its scales likewise, and no more differing codes than the FP8 form."""
+    wl, d, runner, C13, h, host, tile_m = layer
+    S, I, BM = wl.S, wl.I, wl.block_m
+    runner.exact_dot = True
+    try:
+        runner.stage_w13()
+        torch.cuda.synchronize()
+        hq_x = u8_bits(runner.hq)
+        hs_x = np.ascontiguousarray(runner.hs.cpu().numpy())
+    finally:
+        runner.exact_dot = False
+    tiles = tile_map(host["eids"], host["ntpp"], BM, tile_m, I // 128)
+    picked = pick_tiles(tiles, host["sorted"], S)
+    n = nd = nd_fp8 = 0
+    for name, ti in picked.items():
+        pos = tile_positions(ti, host["sorted"], S)
+        _, _, _, _, qref, sref = _fused_ref(layer, name, ti)
+        cols = np.r_[128 * ti.j:128 * ti.j + 128]
+        dx = e4m3_ulp_diff(hq_x[pos][:, cols], qref)
+        df = e4m3_ulp_diff(host["hq"][pos][:, cols], qref)
+        s_diff = hs_x[pos][:, ti.j:ti.j + 1] != sref
+        print(f"  exact W13 {name}: {int((dx > 0).sum())} of {dx.size} codes differ (max {int(dx.max())} ulp), "
+              f"{int(s_diff.sum())} scales; FP8 form {int((df > 0).sum())}", flush=True)
+        assert dx.max() <= A7_MAX_ULP, f"exact W13 tile {name}: a code {int(dx.max())} ulp off"
+        assert s_diff.mean() <= A7_MAX_FRAC, f"exact W13 tile {name}: {int(s_diff.sum())} scales differ"
+        n += dx.size
+        nd += int((dx > 0).sum())
+        nd_fp8 += int((df > 0).sum())
+    assert nd <= A7_MAX_FRAC * n, f"{wl.name}: {nd} of {n} exact-mode codes differ"
+    assert nd <= nd_fp8

@@ -25,13 +25,17 @@ def test_m1_spec_meets_worker_fp8_contract():
     assert spec.weight_dtype == "fp8" and spec.act_quant == "group128"
     assert spec.requires_nvshmem is False
     assert builder is schemes.build
-    assert set(spec.tunables_schema) == {"block_m", "n_chunks", "n_streams", "n_chunks_gateup", "n_chunks_down"}
+    assert set(spec.tunables_schema) == {"block_m", "n_chunks", "n_streams", "n_chunks_gateup", "n_chunks_down",
+                                         "exact_dot"}
 
 
 def test_validate_tunables_defaults_and_errors():
     spec = schemes.SPEC
     assert schemes.validate_tunables(spec, {}) == {"block_m": 0, "n_chunks": 1, "n_streams": 1,
-                                                   "n_chunks_gateup": 0, "n_chunks_down": 0}
+                                                   "n_chunks_gateup": 0, "n_chunks_down": 0, "exact_dot": False}
+    assert schemes.validate_tunables(spec, {"exact_dot": True})["exact_dot"] is True
+    with pytest.raises(schemes.SchemeConfigError, match="expected bool"):
+        schemes.validate_tunables(spec, {"exact_dot": 1})
     assert schemes.validate_tunables(spec, {"n_chunks": 4})["n_chunks"] == 4
     with pytest.raises(schemes.SchemeConfigError, match="violate schema"):
         schemes.validate_tunables(spec, {"bogus": 1})
@@ -57,6 +61,11 @@ def test_build_scheme_rejects_unknown_code_bad_context_and_missing_data():
         with pytest.raises(schemes.SchemeConfigError, match="n_chunks"):
             schemes.build_scheme(None, SimpleNamespace(world_size=1), object(),
                                  SimpleNamespace(code="m1", tunables=bad))
+    # the exact-dot mode belongs to the fused W13, which the K-split structure does not run
+    with pytest.raises(schemes.SchemeConfigError, match="exact_dot"):
+        schemes.build_scheme(None, SimpleNamespace(world_size=1), object(),
+                             SimpleNamespace(code="m1", tunables={"n_chunks_gateup": 2, "n_chunks_down": 4,
+                                                                  "exact_dot": True}))
 
 
 @pytest.mark.parametrize("name", SCRIPTS)
