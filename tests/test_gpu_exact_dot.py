@@ -148,3 +148,68 @@ def test_exact_mode_through_the_scheme():
     r = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, k, BM, exact_dot=True)
     np.testing.assert_array_equal(y, bf16_bits(r.run(g["x"], g["topk_w"], g["topk_ids"])))
     inst.close()
+
+
+def test_exact_mode_chunked_and_mapped_paths():
+    """The exact mode through the token-chunk pipeline (scheme tunables
+    n_chunks / n_streams) equals one pass bit for bit, and with an expert map
+    (slots of other devices dropped, expert -1 blocks) it equals the local
+    problem, as the FP8 form does."""
+    from types import SimpleNamespace
+
+    from td_benchmark_amd import ops, schemes
+    T, H, I, E, k, BM = 300, 256, 256, 8, 2, 16
+    _log("exact mode: chunked scheme and expert map")
+    c = make_case(T, H, I, E, k, BM, seed=33)
+    g = to_gpu(c)
+    one = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, k, BM, exact_dot=True)
+    y_one = bf16_bits(one.run(g["x"], g["topk_w"], g["topk_ids"]))
+    ckpt = SimpleNamespace(w1=SimpleNamespace(fp8=g["w13"], scale=g["w13_s"]),
+                           w2=SimpleNamespace(fp8=g["w2"], scale=g["w2_s"]))
+    routing = SimpleNamespace(topk_ids_full=g["topk_ids"].view(T, k), topk_weights_full=g["topk_w"].view(T, k))
+    data = SimpleNamespace(ckpt=ckpt, hidden_local=g["x"], routing=routing)
+    inst = schemes.build_scheme(None, SimpleNamespace(world_size=1), data,
+                                SimpleNamespace(code="m1", tunables={"block_m": BM, "n_chunks": 3, "n_streams": 2,
+                                                                     "exact_dot": True}))
+    np.testing.assert_array_equal(bf16_bits(inst.run()), y_one)
+    inst.close()
+    # expert map: local experts 2, 5, 6
+    local = [2, 5, 6]
+    emap = np.full(E, -1, np.int32)
+    emap[local] = np.arange(len(local), dtype=np.int32)
+    em = torch.from_numpy(emap).cuda()
+    sub = {n: g[n][local].contiguous() for n in ("w13", "w13_s", "w2", "w2_s")}
+    ep = ops.FusedExpertsRunner(sub["w13"], sub["w13_s"], sub["w2"], sub["w2_s"], T, k, BM, global_num_experts=E,
+                                expert_map=em, exact_dot=True)
+    y_ep = bf16_bits(ep.run(g["x"], g["topk_w"], g["topk_ids"]))
+    ids_local = torch.from_numpy(emap[c.topk_ids]).cuda()
+    loc = ops.FusedExpertsRunner(sub["w13"], sub["w13_s"], sub["w2"], sub["w2_s"], T, k, BM, exact_dot=True)
+    loc.D.zero_()
+    y_loc = bf16_bits(loc.run(g["x"], g["topk_w"].view(-1), ids_local.view(-1)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y_ep, y_loc)
+
+
+def test_exact_mode_at_a_ragged_width():
+    """H = 300 (zero-padded to 384 inside the runner) in exact mode equals the
+    first H columns of the explicitly padded layer in exact mode."""
+    from td_benchmark_amd import ops
+    T, H, I, E, k, BM = 128, 300, 256, 16, 4, 32
+    _log("exact mode at H=300")
+    c = make_case(T, H, I, E, k, BM, seed=5, routing="zipf")
+    g = to_gpu(c)
+    Hp = 384
+    r = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, k, BM, exact_dot=True)
+    y = bf16_bits(r.run(g["x"], g["topk_w"], g["topk_ids"]))
+    x = np.zeros((T, Hp), np.uint16)
+    x[:, :H] = c.x
+    w13 = np.zeros(c.w13_q.shape[:2] + (Hp,), np.uint8)
+    w13[:, :, :H] = c.w13_q
+    w2 = np.zeros((E, Hp, I), np.uint8)
+    w2[:, :H] = c.w2_q
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    rp = ops.FusedExpertsRunner(dev(w13).view(ops.FP8), g["w13_s"], dev(w2).view(ops.FP8), g["w2_s"], T, k, BM,
+                                exact_dot=True)
+    yp = bf16_bits(rp.run(dev(x.view(np.int16)).view(torch.bfloat16), g["topk_w"], g["topk_ids"]))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y, yp[:, :H])
