@@ -927,7 +927,11 @@ void w13_exact_kernel(GemmArgs g) {
 template <int BM, bool FUSED, bool EXACT>
 static int launch_gemm(const GemmArgs& args, hipStream_t st) {
   using T = Tile<BM>;
-  const void* fn = EXACT ? (const void*)w13_exact_kernel<BM> : (const void*)grouped_gemm_kernel<BM, FUSED>;
+  const void* fn;
+  if constexpr (EXACT)
+    fn = (const void*)w13_exact_kernel<BM>;
+  else
+    fn = (const void*)grouped_gemm_kernel<BM, FUSED>;
   // Set once per process (a function-local static is initialised exactly once,
   // also when several host threads make their first call together).
   static const hipError_t attr_rc =
