@@ -1188,8 +1188,13 @@ static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const
   if (top_k <= 0) return kErrBadTopK;
   if (E <= 0) return kErrBadExperts;
   if (!block_m_ok(BM)) return kErrBadBlockSize;
-  const int TM = resolve_tile_m(tile_m, BM, S, E);
+  int TM = resolve_tile_m(tile_m, BM, S, E);
   if (TM < 0) return kErrBadBlockSize;
+  // The exact-dot form runs a 256-row tile as two 128-row bodies one after the
+  // other; its automatic tile is 128 rows where the align block allows it
+  // (separate 128-row workgroups measured 6-10 % faster on DeepSeek-V3 and
+  // Mixtral).  Results do not depend on the tile height.
+  if (exact && tile_m == 0 && TM == 256 && BM <= 128) TM = 128;
   if (max_padded == 0 || S == 0) return kOk;
   if (!Aq || !A_scale || !W13 || !W13_scale || !sorted_ids || !expert_ids || !ntpp || !hq || !hs)
     return kErrNullPointer;

@@ -622,11 +622,14 @@ class SharedExpertRunner:
     contract of schemes/base.py:45-93): the align outputs exist for
     ``max_tokens`` rows and for each count in ``row_counts``, or added later
     with ``prepare(rows)``; a call with any other row count raises instead of
-    allocating."""
+    allocating.
+
+    ``exact_dot`` selects the exact-dot W13 (as FusedExpertsRunner's; a
+    layer runner with a shared expert sets it to its own mode on every run)."""
 
     def __init__(self, w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, max_tokens: int, block_size_m: int | None = None,
-                 row_counts: tuple[int, ...] = ()):
+                 row_counts: tuple[int, ...] = (), exact_dot: bool = False):
         E1, N2, H = _need_weights(w1, w1_scale, "w1")
         _need_weights(w2, w2_scale, "w2")
         if E1 != 1 or w2.shape[0] != 1:
@@ -636,6 +639,7 @@ class SharedExpertRunner:
         if (N2 // 2) % 128:
             raise ValueError(f"the intermediate size {N2 // 2} must be a multiple of 128")
         self.H, self.I, self.max_tokens = H, N2 // 2, max_tokens
+        self.exact_dot = bool(exact_dot)
         self.Hp = _blocks128(H) * 128
         w1, w2 = _pad_fp8(w1, 2, self.Hp), _pad_fp8(w2, 1, self.Hp)
         self.w1, self.w1_scale, self.w2, self.w2_scale = w1, w1_scale, w2, w2_scale
@@ -688,10 +692,17 @@ class SharedExpertRunner:
         _need(q, "x", FP8, (rows, self.Hp))
         _need(s, "input_scale", torch.float32, (rows, self.Hp // 128))
         a = self._align_for(rows)
-        check(lib().moe_gemm_w13_silu_quant(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
-                                            _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
-                                            self.Hp, self.I, 1, self.BM, a.max_padded, _ptr(self.hq),
-                                            _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
+        if self.exact_dot:
+            check(lib().moe_gemm_w13_silu_quant_exact(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
+                                                      _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
+                                                      self.Hp, self.I, 1, self.BM, a.max_padded, 0, 0,
+                                                      _ptr(self.hq), _ptr(self.hs), _stream()),
+                  "moe_gemm_w13_silu_quant_exact")
+        else:
+            check(lib().moe_gemm_w13_silu_quant(_ptr(q), _ptr(s), _ptr(self.w1), _ptr(self.w1_scale),
+                                                _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), rows, 1,
+                                                self.Hp, self.I, 1, self.BM, a.max_padded, _ptr(self.hq),
+                                                _ptr(self.hs), _stream()), "moe_gemm_w13_silu_quant")
         out = self.out[:rows]
         check(lib().moe_grouped_gemm(_ptr(self.hq), _ptr(self.hs), _ptr(self.w2), _ptr(self.w2_scale),
                                      _ptr(a.sorted_ids), _ptr(a.expert_ids), _ptr(a.ntpp), None, rows, 1, 1,
@@ -736,7 +747,7 @@ class FusedExpertsRunner:
     on the bf16 matrix core, about twice the matrix-core time of the FP8
     instruction, whose in-group product truncation otherwise moves about
     0.2 % of the intermediate codes.  W2 and every other stage are the same
-    in both modes."""
+    in both modes, and a shared expert follows the layer's mode."""
 
     def __init__(self, w13: torch.Tensor, w13_scale: torch.Tensor, w2: torch.Tensor,
                  w2_scale: torch.Tensor, num_tokens: int, top_k: int, block_size_m: int | None = None,
@@ -870,8 +881,10 @@ class FusedExpertsRunner:
               "moe_grouped_gemm")
 
     def stage_shared(self) -> None:
-        """The shared expert on the layer's own FP8 input (no second quant)."""
+        """The shared expert on the layer's own FP8 input (no second quant),
+        in the layer's W13 mode."""
         if self.shared is not None:
+            self.shared.exact_dot = self.exact_dot
             self.shared_out = self.shared(self.q1, self.s1)
 
     def stage_reduce(self) -> None:

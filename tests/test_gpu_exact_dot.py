@@ -213,3 +213,36 @@ def test_exact_mode_at_a_ragged_width():
     yp = bf16_bits(rp.run(dev(x.view(np.int16)).view(torch.bfloat16), g["topk_w"], g["topk_ids"]))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y, yp[:, :H])
+
+
+def test_exact_shared_expert_meets_the_bar_and_follows_the_layer():
+    """The shared expert (E = 1, top-1) in exact mode: its intermediate codes
+    within the north-star bar of the oracle chain; a layer runner in exact mode
+    runs its shared expert in exact mode too."""
+    from td_benchmark_amd import ops
+    T, H, I = 512, 1024, 512
+    _log(f"exact shared expert T={T} H={H} I={I}")
+    rng = np.random.default_rng(21)
+    x = oracle.f32_to_bf16(rng.standard_normal((T, H), dtype=np.float32))
+    w1q, w1s = oracle.quant_block128((rng.standard_normal((1, 2 * I, H)) * H ** -0.5).astype(np.float32))
+    w2q, w2s = oracle.quant_block128((rng.standard_normal((1, H, I)) * I ** -0.5).astype(np.float32))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    sh = ops.SharedExpertRunner(dev(w1q).view(ops.FP8), dev(w1s), dev(w2q).view(ops.FP8), dev(w2s), T,
+                                exact_dot=True)
+    sh(dev(x.view(np.int16)).view(torch.bfloat16))
+    torch.cuda.synchronize()
+    st = oracle.moe_layer_stages(x, np.zeros((T, 1), np.int32), np.ones((T, 1), np.float32), w1q, w1s, w2q, w2s,
+                                 sh.BM)
+    d = e4m3_ulp_diff(u8_bits(sh.hq)[:T], st["q2"])       # one expert, top-1: position p holds slot p
+    s_diff = sh.hs.cpu().numpy()[:T] != st["s2"]
+    print(f"  shared exact: {int((d > 0).sum())} of {d.size} codes differ (max {int(d.max())} ulp), "
+          f"{int(s_diff.sum())} scales", flush=True)
+    assert (d > 0).mean() <= A7_MAX_FRAC and d.max() <= A7_MAX_ULP and s_diff.mean() <= A7_MAX_FRAC
+    # a layer runner in exact mode sets its shared expert's mode
+    c = make_case(T, H, I, 8, 2, 64, seed=2)
+    g = to_gpu(c)
+    sh.exact_dot = False
+    r = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, 2, 64, shared=sh, exact_dot=True)
+    r.run(g["x"], g["topk_w"], g["topk_ids"])
+    torch.cuda.synchronize()
+    assert sh.exact_dot
