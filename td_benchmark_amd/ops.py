@@ -1080,14 +1080,15 @@ def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tenso
                   topk_weights: torch.Tensor, topk_ids: torch.Tensor, global_num_experts: int = -1,
                   w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
                   block_size_m: int | None = None, quant_config: Any = None,
-                  expert_map: torch.Tensor | None = None) -> torch.Tensor:
+                  expert_map: torch.Tensor | None = None, exact_dot: bool = False) -> torch.Tensor:
     """vLLM ``fused_experts`` as the reference calls it (schemes/vllm_tp.py:
     52-60; with ``expert_map`` for expert parallelism, schemes/vllm_ep.py:
     57-66) for FP8 w8a8 with [128,128] weight blocks.  Scales come either as
     keywords or from ``quant_config`` (attributes ``w1_scale``/``w2_scale``).
     With an expert map, w1/w2 hold the local experts and slots routed to other
-    devices contribute zeros.  Allocates per call; prebuild a
-    FusedExpertsRunner for timed loops."""
+    devices contribute zeros.  ``exact_dot`` selects the exact-dot W13
+    (FusedExpertsRunner).  Allocates per call; prebuild a FusedExpertsRunner
+    for timed loops."""
     if quant_config is not None:
         w1_scale = getattr(quant_config, "w1_scale", w1_scale)
         w2_scale = getattr(quant_config, "w2_scale", w2_scale)
@@ -1096,6 +1097,6 @@ def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tenso
     T, k = topk_ids.shape
     gne = None if global_num_experts in (-1, None) else global_num_experts
     runner = FusedExpertsRunner(w1, w1_scale, w2, w2_scale, T, k, block_size_m,
-                                global_num_experts=gne, expert_map=expert_map)
+                                global_num_experts=gne, expert_map=expert_map, exact_dot=exact_dot)
     return runner.run(hidden_states.contiguous(), topk_weights.contiguous().view(-1),
                       topk_ids.contiguous().view(-1)).clone()

@@ -148,6 +148,10 @@ def test_exact_mode_through_the_scheme():
     r = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], T, k, BM, exact_dot=True)
     np.testing.assert_array_equal(y, bf16_bits(r.run(g["x"], g["topk_w"], g["topk_ids"])))
     inst.close()
+    # and through fused_experts, the vLLM-shaped entry
+    y_fe = ops.fused_experts(g["x"], g["w13"], g["w2"], g["topk_w"].view(T, k), g["topk_ids"].view(T, k),
+                             w1_scale=g["w13_s"], w2_scale=g["w2_s"], block_size_m=BM, exact_dot=True)
+    np.testing.assert_array_equal(bf16_bits(y_fe), y)
 
 
 def test_exact_mode_chunked_and_mapped_paths():
