@@ -23,7 +23,8 @@ from hypothesis import given, settings
 from hypothesis import strategies as st
 
 import oracle
-from moe_cases import a7_account, a7_assert, bf16_bits, dequant_weights_f32, make_case, to_gpu, u8_bits
+from moe_cases import (A7_MAX_FRAC, A7_MAX_ULP, a7_account, a7_assert, bf16_bits, dequant_weights_f32, e4m3_ulp_diff,
+                       make_case, to_gpu, u8_bits)
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -238,3 +239,38 @@ def test_random_fused_w13_equals_the_unfused_chain(case):
     rep = a7_account(hq_np, hs_np, bf16_bits(h)[slots], bf16_bits(C)[slots], st_["q2"][slots], st_["s2"][slots],
                      st_["h"][slots], st_["c13"][slots], st_["c13_f32"][slots], st_["bound13"][slots])
     a7_assert(rep, f"random fused W13 {case}")
+
+
+@settings(max_examples=30, deadline=None, derandomize=True)
+@given(fused_cases())
+def test_random_exact_w13_meets_the_code_bar(case):
+    """The exact-dot W13 (moe_gemm_w13_silu_quant_exact) at every drawn shape
+    and tile height: its codes against the CPU chain (exact dots,
+    overlap/kernels.py:172-179, then overlap_forward.py:277-284) differ by at
+    most 1 ULP, on at most 0.1 % of the codes (at least one code allowed, for
+    the smallest draws), and no more often than the FP8 form's."""
+    from td_benchmark_amd import ops
+
+    print(f"case: random exact W13 {case}", flush=True)
+    T, H, I, E, k, BM, tm = (case[x] for x in ("T", "H", "I", "E", "k", "BM", "tile_m"))
+    c = make_case(T, H, I, E, k, BM, seed=case["seed"], routing=case["routing"])
+    g = to_gpu(c)
+    q1, s1 = ops.per_token_group_quant_fp8(g["x"])
+    sorted_ids, eids, ntpp = ops.moe_align_block_size(g["topk_ids"], BM, E)
+    hq_x, hs_x = ops.gemm_w13_silu_quant(q1, s1, g["w13"], g["w13_s"], sorted_ids, eids, ntpp, c.S, k, BM,
+                                         tile_m=tm, exact_dot=True)
+    hq_f, _ = ops.gemm_w13_silu_quant(q1, s1, g["w13"], g["w13_s"], sorted_ids, eids, ntpp, c.S, k, BM, tile_m=tm)
+    torch.cuda.synchronize()
+    n = int(ntpp.item())
+    srt = sorted_ids.cpu().numpy()[:n]
+    pos = np.nonzero(srt < c.S)[0]
+    slots = srt[pos]
+    st_ = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, BM)
+    d = e4m3_ulp_diff(u8_bits(hq_x)[pos], st_["q2"][slots])
+    df = e4m3_ulp_diff(u8_bits(hq_f)[pos], st_["q2"][slots])
+    s_diff = hs_x.cpu().numpy()[pos] != st_["s2"][slots]
+    nd = int((d > 0).sum())
+    assert d.max() <= A7_MAX_ULP, (case, int(d.max()))
+    assert nd <= max(1, A7_MAX_FRAC * d.size), (case, nd, d.size)
+    assert int(s_diff.sum()) <= max(1, A7_MAX_FRAC * s_diff.size), (case, int(s_diff.sum()))
+    assert nd <= max(1, int((df > 0).sum())), (case, nd, int((df > 0).sum()))
