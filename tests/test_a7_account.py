@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from moe_cases import A7_GT1_MAX_REL_AMAX, A7_MFMA_MAX_ULP, a7_account, a7_assert, make_case
+from moe_cases import A7_GT1_MAX_REL_AMAX, A7_MFMA_MAX_ULP, a7_account, a7_assert, count_bar, make_case
 
 
 @pytest.fixture(scope="module")
@@ -47,8 +47,9 @@ def test_multi_ulp_code_at_large_h_fails(chain):
 
 
 def test_code_beyond_the_ulp_cap_fails(chain):
-    """A code near zero (|h| below 2^-12 of its group's amax, where multi-ULP
-    moves are allowed) moved beyond the cap fails on the cap alone."""
+    """A code near zero (|h| below A7_GT1_MAX_REL_AMAX of its group's amax,
+    where multi-ULP moves are allowed) moved beyond the cap fails on the cap
+    alone."""
     h32 = np.abs(oracle.bf16_to_f32(chain["h"])).astype(np.float64)
     amax = np.repeat(h32.reshape(h32.shape[0], -1, 128).max(axis=2), 128, axis=1)
     rel = np.where((chain["q2"] & 0x7F) > A7_MFMA_MAX_ULP + 1, h32 / np.maximum(amax, 1e-30), np.inf)
@@ -61,3 +62,11 @@ def test_code_beyond_the_ulp_cap_fails(chain):
     assert rep["max_ulp"] == A7_MFMA_MAX_ULP + 1 and rep["gt1_max_rel_to_amax"] <= A7_GT1_MAX_REL_AMAX
     with pytest.raises(AssertionError, match="ulp cap"):
         a7_assert(rep, "planted code beyond the cap")
+
+
+def test_count_bar_known_answers():
+    """The Poisson bar for rare events: one event always allowed, about
+    mean + 3 sigma for large samples."""
+    assert count_bar(1e-3, 0) == 1.0
+    assert abs(count_bar(1e-3, 10 ** 6) - (1000 + 3 * 1000 ** 0.5 + 1)) < 1e-9
+    assert 5 < count_bar(1e-3, 1251) < 6

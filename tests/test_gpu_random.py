@@ -23,8 +23,8 @@ from hypothesis import given, settings
 from hypothesis import strategies as st
 
 import oracle
-from moe_cases import (A7_MAX_FRAC, A7_MAX_ULP, a7_account, a7_assert, bf16_bits, dequant_weights_f32, e4m3_ulp_diff,
-                       make_case, to_gpu, u8_bits)
+from moe_cases import (A7_MAX_FRAC, A7_MAX_ULP, a7_account, a7_assert, bf16_bits, count_bar, dequant_weights_f32,
+                       e4m3_ulp_diff, make_case, to_gpu, u8_bits)
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -248,7 +248,9 @@ def test_random_exact_w13_meets_the_code_bar(case):
     and tile height: its codes against the CPU chain (exact dots,
     overlap/kernels.py:172-179, then overlap_forward.py:277-284) differ by at
     most 1 ULP, on at most 0.1 % of the codes (at least one code allowed, for
-    the smallest draws), and no more often than the FP8 form's."""
+    the smallest draws), and no more often than the FP8 form's; its group
+    scales differ where the amax element's C13 rounds the other way, on at
+    most 0.1 % of the groups (Poisson slack, tests/moe_cases.py count_bar)."""
     from td_benchmark_amd import ops
 
     print(f"case: random exact W13 {case}", flush=True)
@@ -272,5 +274,5 @@ def test_random_exact_w13_meets_the_code_bar(case):
     nd = int((d > 0).sum())
     assert d.max() <= A7_MAX_ULP, (case, int(d.max()))
     assert nd <= max(1, A7_MAX_FRAC * d.size), (case, nd, d.size)
-    assert int(s_diff.sum()) <= max(1, A7_MAX_FRAC * s_diff.size), (case, int(s_diff.sum()))
+    assert int(s_diff.sum()) <= count_bar(A7_MAX_FRAC, s_diff.size), (case, "scales", int(s_diff.sum()))
     assert nd <= max(1, int((df > 0).sum())), (case, nd, int((df > 0).sum()))
