@@ -574,8 +574,13 @@ def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, i
     DeepSeek-V3, Mixtral, Qwen3-30B-A3B and the reference's v1 GroupGEMM
     sweep, 4-1024 rows per expert):
 
-    * avg <= 40: 32.  The layer streams its weights; the 32-row tile streams
+    * avg <= 28: 32.  The layer streams its weights; the 32-row tile streams
       them faster than the 16-row one and wastes less than taller blocks.
+    * avg <= 44: 64.  Most experts now fill a 32-row block and spill into a
+      second one; 64-row blocks keep them in one tile (40 rows per expert:
+      DeepSeek-V3 2151 us against 2588 at 32, Mixtral 336 against 402,
+      Qwen3 161 against 176, v1 186 against 198; within 2 % of the best
+      block size on all four shapes at 32 and 40 rows).
     * avg <= 100: 128.  Most experts fit one block; a 128-row tile reads
       fewer LDS bytes per MFMA than a 64-row one (v1 shape, 64 rows per
       expert: 195 us against 209 at 64; DeepSeek-V3: 2208 against 2606).
@@ -586,8 +591,10 @@ def get_moe_config(num_tokens: int, num_experts: int, top_k: int) -> dict[str, i
       a second 256-row block and 128-row blocks split them evenly over two
       256-row tiles instead (DeepSeek-V3 at 256: 3920 against 4058 us)."""
     avg = num_tokens * top_k / max(num_experts, 1)
-    if avg <= 40:
+    if avg <= 28:
         bm = 32
+    elif avg <= 44:
+        bm = 64
     elif avg <= 100:
         bm = 128
     elif 240 <= avg <= 288:

@@ -22,7 +22,10 @@ def test_moe_config_block_m_tracks_rows_per_expert():
     assert ops.get_moe_config(8192, 256, 8)["BLOCK_SIZE_M"] == 128
     # decode: 128*8/256 = 4 rows per expert -> 32 (its weight stream is faster than 16's)
     assert ops.get_moe_config(128, 256, 8)["BLOCK_SIZE_M"] == 32
-    assert ops.get_moe_config(64, 4, 2)["BLOCK_SIZE_M"] == 32   # 32 rows per expert
+    assert ops.get_moe_config(48, 4, 2)["BLOCK_SIZE_M"] == 32   # 24 rows per expert
+    assert ops.get_moe_config(64, 4, 2)["BLOCK_SIZE_M"] == 64   # 32 rows per expert
+    assert ops.get_moe_config(1280, 256, 8)["BLOCK_SIZE_M"] == 64  # 40 rows per expert (DeepSeek-V3 shape)
+    assert ops.get_moe_config(1536, 256, 8)["BLOCK_SIZE_M"] == 128  # 48
     assert ops.get_moe_config(512, 64, 8)["BLOCK_SIZE_M"] == 128  # 64 rows per expert
     assert ops.get_moe_config(1024, 64, 8)["BLOCK_SIZE_M"] == 256  # 128: one tile per expert
     assert ops.get_moe_config(2560, 64, 8)["BLOCK_SIZE_M"] == 256  # 320
