@@ -18,7 +18,9 @@ sample of the same workload.  ``shared_expert`` times the shared expert (one
 E=1, top-1 expert of the same hidden and intermediate size) on the layer's own
 FP8 input, outside the layer time.  ``power`` gives socket power, graphics
 clock and energy per call of the layer, W13 and W2, each run back to back
-for a few seconds (amd-smi; null where it is unavailable).
+for a few seconds (amd-smi; null where it is unavailable).  ``exact_dot``
+times the layer with W13 in its opt-in exact-dot mode (the FP8 codes on the
+bf16 matrix core); the headline numbers are the FP8 form.
 """
 from __future__ import annotations
 
