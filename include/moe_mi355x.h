@@ -230,8 +230,9 @@ int moe_gemm_w13_silu_quant_pos(const void* Aq, const float* A_scale_pos, const 
  * of the bf16 C13 values across a rounding boundary and about 0.2 % of the
  * intermediate codes by up to a few ULPs.  This variant converts the FP8
  * codes exactly to bf16 and takes every 128-element dot as four bf16 MFMAs,
- * whose products are exact, at about twice the matrix-core time of the FP8
- * form.  Same arguments and outputs as moe_gemm_w13_silu_quant_tiled with
+ * whose products are exact, and applies the scales as the reference does,
+ * acc + (dot * a_scale) * b_scale with each operation rounded in fp32, at
+ * about twice the matrix-core time of the FP8 form.  Same arguments and outputs as moe_gemm_w13_silu_quant_tiled with
  * scales_by_position == 0, and as moe_gemm_w13_silu_quant_pos (A_scale and
  * hs K-major by sorted position) with scales_by_position != 0. */
 int moe_gemm_w13_silu_quant_exact(const void* Aq, const float* A_scale, const void* W13,

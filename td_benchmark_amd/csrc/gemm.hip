@@ -608,10 +608,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
         };
         constexpr int NQ = 2 * T::CS;  // weight fragments per step
         if constexpr (EXACT) {
+#pragma clang fp contract(off)
           // Exact dots on the bf16 matrix core: the step's A fragments are
           // converted once, each weight fragment as it is read; every 128-K
-          // dot is four chained bf16 MFMAs, then scaled into acc as below.
-          scale_products();
+          // dot is four chained bf16 MFMAs.  The dot is scaled into acc by the
+          // reference's own chain, acc + (dot * a_s) * b_s with three
+          // roundings (overlap/kernels.py:179), not the fused form below: with
+          // exact dots the scale chain is the main remaining difference from
+          // the reference's arithmetic (it moves about 20x more C13 values).
+          float sa[RA];
+#pragma unroll
+          for (int r = 0; r < RA; ++r) sa[r] = tSA[r * 16];
+          const float sbg[2] = {smSB[kk], smSB[kMaxKB + kk]};
           v8bf abf[RA][4];
           [&]<int... R>(std::integer_sequence<int, R...>) {
             (
@@ -634,8 +642,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t j, int64_t 
                   for (int r = 0; r < RA; ++r) {
                     const v4f p = mfma_bf16_dot128(bbf, abf[r]);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                      acc[r][gq][cq][v] = __builtin_fmaf(p[v], sab[gq][r], acc[r][gq][cq][v]);
+                    for (int v = 0; v < 4; ++v) {
+                      float t = p[v] * sa[r];
+                      t = t * sbg[gq];
+                      acc[r][gq][cq][v] = acc[r][gq][cq][v] + t;
+                    }
                   }
                 }(),
                 ...);

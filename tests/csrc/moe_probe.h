@@ -19,6 +19,9 @@
  *      v_mfma_f32_16x16x32_bf16, the accumulator chained through the
  *      instruction: the exact-dot form of moe_gemm_w13_silu_quant_exact,
  *      through the same code
+ *   5  (moe_probe_block_gemm only) form 4's dots with the reference's scale
+ *      chain, acc = acc + (dot * a_s) * b_s, three roundings, in place of
+ *      fma(dot, a_s * b_s, acc)
  */
 #ifndef MOE_PROBE_H
 #define MOE_PROBE_H

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(64) void block_gemm_kernel(const uint8_t* __restric
                                                         const uint8_t* __restrict__ B, const float* __restrict__ Bs,
                                                         int64_t N, int64_t K, int form,
                                                         uint16_t* __restrict__ C) {
+#pragma clang fp contract(off)
   const int lane = threadIdx.x, fr = lane & 15, kseg = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.y * 16, n0 = (int64_t)blockIdx.x * 16;
   const int64_t KB = K / 128;
@@ -98,10 +99,22 @@ __global__ __launch_bounds__(64) void block_gemm_kernel(const uint8_t* __restric
     const v8i fa = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
     const v8i fb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
     // weight fragment first: lane (fr, kseg) holds token fr, columns 4 kseg + v
-    const v4f p = dot_form(fb, fa, form);
-    const float sab = As[(m0 + fr) * KB + kb] * Bs[(n0 / 128) * KB + kb];
+    const v4f p = dot_form(fb, fa, form == 5 ? 4 : form);
+    const float sa = As[(m0 + fr) * KB + kb], sb = Bs[(n0 / 128) * KB + kb];
+    if (form == 5) {
+      // the reference's chain, acc += dot * a_s * b_s with three roundings
+      // (overlap/kernels.py:179), in place of the kernel's fma(dot, a_s * b_s, acc)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(p[v], sab, acc[v]);
+      for (int v = 0; v < 4; ++v) {
+        float t = p[v] * sa;
+        t = t * sb;
+        acc[v] = acc[v] + t;
+      }
+    } else {
+      const float sab = sa * sb;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(p[v], sab, acc[v]);
+    }
   }
   v2u pk;
   pk[0] = pack_bf16x2(acc[0], acc[1]);
@@ -180,7 +193,7 @@ extern "C" int moe_probe_mfma_dot(const void* A, const void* B, float* C, int64_
 extern "C" int moe_probe_block_gemm(const void* A, const float* As, const void* B, const float* Bs, int64_t M,
                                     int64_t N, int64_t K, int32_t form, void* C, void* stream) {
   if (!A || !As || !B || !Bs || !C) return kErrNullPointer;
-  if (M <= 0 || N <= 0 || K <= 0 || M % 16 || N % 16 || K % 128 || form < 0 || form > 4) return kErrBadShape;
+  if (M <= 0 || N <= 0 || K <= 0 || M % 16 || N % 16 || K % 128 || form < 0 || form > 5) return kErrBadShape;
   if (M / 16 > 65535 || N / 16 > (int64_t)1 << 30) return kErrBadShape;
   if (((uintptr_t)A & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 7)) return kErrBadShape;
   hipLaunchKernelGGL(block_gemm_kernel, dim3((unsigned)(N / 16), (unsigned)(M / 16)), dim3(64), 0,

@@ -27,6 +27,7 @@ FORM_K32_CHAINED = 1   # four 16x16x32, accumulator chained through the instruct
 FORM_K32_FP32 = 2      # four 16x16x32 from zero, fp32 adds
 FORM_K128_QUARTERS = 3 # four 16x16x128 with one K quarter each, fp32 adds
 FORM_BF16 = 4          # codes converted to bf16, four 16x16x32 bf16 MFMAs chained
+FORM_BF16_REF_CHAIN = 5  # form 4 with the reference's scale chain (block GEMM only)
 FP8_FORMS = {FORM_K128: "16x16x128", FORM_K32_CHAINED: "4x16x16x32 chained",
              FORM_K32_FP32: "4x16x16x32 + fp32 adds", FORM_K128_QUARTERS: "4x16x16x128 quarters + fp32 adds"}
 FORMS = {**FP8_FORMS, FORM_BF16: "bf16 4x16x16x32"}

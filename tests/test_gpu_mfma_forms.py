@@ -272,6 +272,32 @@ def test_a7_codes_by_dot_form():
              f"C13 {rep.get('c13_diff_frac', 0):.3e}; model chain: C13 {c13_same:.6f} codes {code_same:.6f}")
 
 
+def test_bf16_dots_with_the_reference_scale_chain():
+    """With exact (bf16) dots, the scale chain is what remains between the
+    kernel and the reference's arithmetic: fma(dot, a_s * b_s, acc) moves
+    about 20 times more C13 values off the oracle chain than the reference's
+    acc + (dot * a_s) * b_s (overlap/kernels.py:179), which the exact-dot
+    W13 therefore uses.  Dense W13 of one expert, two seeds."""
+    from td_benchmark_amd import ops
+    T, H, I = 1024, 2048, 512
+    for seed in (11, 12):
+        c = make_case(T, H, I, 1, 1, 128, seed=seed)
+        st = oracle.moe_layer_stages(c.x, c.topk_ids, c.topk_w, c.w13_q, c.w13_s, c.w2_q, c.w2_s, 128)
+        g = to_gpu(c)
+        q1, s1 = ops.per_token_group_quant_fp8(g["x"])
+        w13, ws = g["w13"][0], g["w13_s"][0].contiguous()
+        flips = {}
+        for form in (probe_lib.FORM_BF16, probe_lib.FORM_BF16_REF_CHAIN):
+            _log(f"bf16 dots, scale chain of form {form}: seed {seed}")
+            C = _block_gemm(q1, s1, w13, ws, form)
+            torch.cuda.synchronize()
+            flips[form] = int((bf16_bits(C) != st["c13"]).sum())
+        _log(f"  C13 off the oracle chain: fma chain {flips[probe_lib.FORM_BF16]}, reference chain "
+             f"{flips[probe_lib.FORM_BF16_REF_CHAIN]} of {T * 2 * I}")
+        assert flips[probe_lib.FORM_BF16_REF_CHAIN] * 5 <= flips[probe_lib.FORM_BF16]
+        assert flips[probe_lib.FORM_BF16_REF_CHAIN] <= 1e-5 * T * 2 * I
+
+
 def test_dot_form_rate():
     """Matrix-core throughput of each form on register operands (one launch
     of 8192 waves x 400 iterations x 8 dots, best of 6)."""
