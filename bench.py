@@ -155,11 +155,13 @@ def shared_expert_leg(runner, wl, steps: int, warmup: int) -> dict:
             "input": "the routed layer's FP8 activations and 1x128 scales (no second quant)"}
 
 
-def exact_dot_leg(runner, step, steps: int, warmup: int, flop_w13: float) -> dict:
+def exact_dot_leg(runner, step, steps: int, warmup: int, flop_w13: float, power_seconds: float = 0.0) -> dict:
     """The layer with the W13 stage in exact-dot mode (every 128-element dot
     as four bf16 MFMAs on the codes converted exactly to bf16): W13 and
-    layer time per call, timed with events like the headline layer.  The
-    headline numbers are the FP8 form; this is the cost of the opt-in mode."""
+    layer time per call, timed with events like the headline layer, and,
+    with ``power_seconds``, the exact W13's socket power and clock as in the
+    power leg.  The headline numbers are the FP8 form; this is the cost of
+    the opt-in mode."""
     import torch
     runner.exact_dot = True
     try:
@@ -177,6 +179,7 @@ def exact_dot_leg(runner, step, steps: int, warmup: int, flop_w13: float) -> dic
             step()
             b.record()
         torch.cuda.synchronize()
+        power = power_leg(runner.stage_w13, power_seconds) if power_seconds > 0 else None
     finally:
         runner.exact_dot = False
     step()  # leave the runner's buffers as the FP8 form writes them
@@ -184,7 +187,7 @@ def exact_dot_leg(runner, step, steps: int, warmup: int, flop_w13: float) -> dic
     w13 = summarize_samples([a.elapsed_time(b) * 1e3 for a, b in ev])
     tflops = flop_w13 / (w13["avg"] / 1e6) / 1e12
     return {"w13_us_stats": w13, "layer_us_stats": summarize_samples([a.elapsed_time(b) * 1e3 for a, b in lev]),
-            "w13_TFLOP/s": tflops, "w13_bf16_mfma_frac": tflops / PEAK_BF16_TFLOPS,
+            "w13_TFLOP/s": tflops, "w13_bf16_mfma_frac": tflops / PEAK_BF16_TFLOPS, "w13_power": power,
             "form": "FP8 codes converted to bf16, four v_mfma_f32_16x16x32_bf16 per 128-element dot"}
 
 
@@ -550,7 +553,8 @@ def main() -> int:
     if not args.no_shared:
         result["shared_expert"] = shared_expert_leg(runner, wl, args.steps, args.warmup)
     if not args.no_exact:
-        result["exact_dot"] = exact_dot_leg(runner, step, args.steps, args.warmup, flop_w13)
+        result["exact_dot"] = exact_dot_leg(runner, step, args.steps, args.warmup, flop_w13,
+                                            args.power_seconds if pipe is None else 0.0)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(data, wl, args.cpu_budget)
         n_rows = min(wl.T, 1024) * wl.top_k
