@@ -251,3 +251,38 @@ def test_exact_shared_expert_meets_the_bar_and_follows_the_layer():
     r.run(g["x"], g["topk_w"], g["topk_ids"])
     torch.cuda.synchronize()
     assert sh.exact_dot
+
+
+def test_exact_layer_graph_replays_equal_eager_runs():
+    """A layer captured in exact-dot mode replays the exact kernels: every
+    replay, with unrelated eager work and a host synchronisation between
+    them, equals the eager exact run bit for bit, and new inputs written into
+    the captured tensors give the eager exact result for them.  The eager
+    FP8-form output differs, so the graph did not record the FP8 W13."""
+    from td_benchmark_amd import ops
+    _log("exact layer graph replay T=120 H=256 I=256 E=8 k=2 BM=32")
+    c = make_case(T=120, H=256, I=256, E=8, k=2, BM=32, seed=46)
+    c2 = make_case(T=120, H=256, I=256, E=8, k=2, BM=32, seed=47)
+    g, g2 = to_gpu(c), to_gpu(c2)
+    eager = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 32, exact_dot=True)
+    y_ref = bf16_bits(eager.run(g["x"], g["topk_w"].view(-1), g["topk_ids"].view(-1)))
+    y_ref2 = bf16_bits(eager.run(g2["x"], g2["topk_w"].view(-1), g2["topk_ids"].view(-1)))
+    eager.exact_dot = False
+    y_fp8 = bf16_bits(eager.run(g["x"], g["topk_w"].view(-1), g["topk_ids"].view(-1)))
+    assert not np.array_equal(y_fp8, y_ref)
+    runner = ops.FusedExpertsRunner(g["w13"], g["w13_s"], g["w2"], g["w2_s"], c.T, c.k, 32, exact_dot=True)
+    x, w, ids = g["x"].clone(), g["topk_w"].view(-1).clone(), g["topk_ids"].view(-1).clone()
+    graph = runner.capture(x, w, ids)
+    for i in range(3):
+        junk = torch.randn(512, 512, device="cuda") @ torch.randn(512, 512, device="cuda")
+        torch.cuda.synchronize()
+        y = graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(y), y_ref), f"replay {i}"
+        del junk
+    x.copy_(g2["x"])
+    w.copy_(g2["topk_w"].view(-1))
+    ids.copy_(g2["topk_ids"].view(-1))
+    y = graph.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(y), y_ref2)
