@@ -156,9 +156,13 @@ struct GemmArgs {
   int64_t N;
   int64_t K;
   int64_t I;
-  int64_t max_blocks;      // align blocks that fit in max_padded
+  int64_t max_blocks;      // (virtual) blocks that fit in max_padded
   int64_t n_tiles;         // 256-column n-tiles
   int bma;                 // rows per align block (block_size_m); a tile spans BM / bma of them
+  // Exact-dot launches only: the tile map counts virtual blocks of bma >> vshift
+  // rows (align block b is virtual blocks b << vshift ..), so 128-row tiles can
+  // run over 256-row align blocks.  0 everywhere else.
+  int vshift;
   int top_k;
   int a_by_pos;
   int E;
@@ -770,7 +774,9 @@ __device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   // [x*C, (x+1)*C), so those row tiles run at the same time on one XCD and
   // fetch the weight tile from HBM once.
   const int ntpp = *g.ntpp;
-  const int64_t n_blocks = ntpp / g.bma;
+  const int vsh = EXACT ? g.vshift : 0;
+  const int64_t vb = (int64_t)g.bma >> vsh;  // rows of a (virtual) block
+  const int64_t n_blocks = ntpp / vb;
   const int64_t total = n_blocks * g.n_tiles;
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   const int64_t pid = blockIdx.x;
@@ -805,21 +811,21 @@ __device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   {
     const int ln = threadIdx.x & 63;
     const int64_t ib = bq - 1 - ln, jf = bq + 1 + ln;
-    e = g.eids[bq];
-    const int xb = ib >= 0 ? g.eids[ib] : 0;
-    const int xf = jf < n_blocks ? g.eids[jf] : 0;
+    e = g.eids[bq >> vsh];
+    const int xb = ib >= 0 ? g.eids[ib >> vsh] : 0;
+    const int xf = jf < n_blocks ? g.eids[jf >> vsh] : 0;
     uint64_t end = __ballot(!(ib >= 0 && xb == e));  // blocks before bq with the same expert
     for (int64_t base = bq - 1 - 64; !end; base -= 64) {
       back += 64;
       const int64_t idx = base - ln;
-      end = __ballot(!(idx >= 0 && g.eids[idx] == e));
+      end = __ballot(!(idx >= 0 && g.eids[idx >> vsh] == e));
     }
     back += __ffsll((unsigned long long)end) - 1;
     end = __ballot(!(jf < n_blocks && xf == e));      // and after it
     for (int64_t base = bq + 1 + 64; !end; base += 64) {
       fwd += 64;
       const int64_t idx = base + ln;
-      end = __ballot(!(idx < n_blocks && g.eids[idx] == e));
+      end = __ballot(!(idx < n_blocks && g.eids[idx >> vsh] == e));
     }
     fwd += __ffsll((unsigned long long)end) - 1;
   }
@@ -831,9 +837,10 @@ __device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   // split over its row tiles as evenly as possible, the larger tiles last:
   // a run of three blocks in 2-block tiles becomes 1 + 2 blocks, two tiles
   // that stream the same weight tiles at the same pace, rather than 2 + 1,
-  // a full tile and a tile of a few padded rows.  Only the last block of a run
-  // holds padding, so a tile's valid rows are still a prefix.
-  const int64_t ub = BM / g.bma;
+  // a full tile and a tile of a few padded rows.  Only the last align block
+  // of a run holds padding, so a tile's valid rows are still a prefix (with
+  // virtual blocks, the run's last one may hold no valid row at all).
+  const int64_t ub = BM / vb;
   const int64_t units = (run + ub - 1) / ub;
   const int64_t in_run = t - b0 * g.n_tiles;
   if (in_run >= units * g.n_tiles) return;
@@ -852,9 +859,9 @@ __device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   const int64_t u = by_col ? in_grp % units : in_grp / gsz;  // row tile of the run
   const int64_t base = run / units, n_short = units - run % units;  // n_short tiles of `base` blocks
   const int64_t b = b0 + (u < n_short ? u * base : n_short * base + (u - n_short) * (base + 1));
-  const int64_t pos0 = b * g.bma;               // sorted position of tile row 0
+  const int64_t pos0 = b * vb;                  // sorted position of tile row 0
   // tile rows that belong to this run (the rest are not read or written)
-  const int rows_avail = (int)((u < n_short ? base : base + 1) * g.bma);
+  const int rows_avail = (int)((u < n_short ? base : base + 1) * vb);
 
   if (e < 0 || e >= g.E) {
     // Expert not local: zero output rows (kernels.py:112-120).
@@ -887,6 +894,19 @@ __device__ __forceinline__ void grouped_gemm_body(const GemmArgs& g) {
   bool row_valid = false;
   if (tid < BM && tid < rows_avail) row_valid = g.sorted[pos0 + tid] < g.S;
   const int nvalid = __syncthreads_count(row_valid);
+  if constexpr (EXACT) {
+    // The second half of a 256-row align block whose slots all sit in its
+    // first half: padding only, written as the zero codes and floor scales
+    // that the two-body tile writes there.
+    if (nvalid == 0) {
+      for (int ci = tid; ci < rows_avail * 8; ci += T::THREADS) {
+        const int row = ci >> 3, cc = ci & 7;
+        *reinterpret_cast<v4i*>(g.hq + (pos0 + row) * g.I + j * 128 + cc * 16) = (v4i){0, 0, 0, 0};
+      }
+      for (int row = tid; row < rows_avail; row += T::THREADS) *hs_at(g, pos0 + row, j) = kScaleFloor;
+      return;
+    }
+  }
   // A tile with few valid rows (an expert's last rows, or a one-block tile of
   // a run split over tiles) runs a shorter body: kTailRows rows, bound by
   // streaming its weight tile with a three-deep LDS ring; or, in a 256-row
@@ -1202,10 +1222,15 @@ static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const
   int TM = resolve_tile_m(tile_m, BM, S, E);
   if (TM < 0) return kErrBadBlockSize;
   // The exact-dot form runs a 256-row tile as two 128-row bodies one after the
-  // other; its automatic tile is 128 rows where the align block allows it
-  // (separate 128-row workgroups measured 6-10 % faster on DeepSeek-V3 and
-  // Mixtral).  Results do not depend on the tile height.
-  if (exact && tile_m == 0 && TM == 256 && BM <= 128) TM = 128;
+  // other; its automatic tile is 128 rows instead (separate 128-row workgroups
+  // measured 6-10 % faster on DeepSeek-V3 and Mixtral), over 256-row align
+  // blocks as two virtual 128-row blocks each.  Results do not depend on the
+  // tile height.
+  int vshift = 0;
+  if (exact && tile_m == 0 && TM == 256) {
+    TM = 128;
+    vshift = BM == 256 ? 1 : 0;
+  }
   if (max_padded == 0 || S == 0) return kOk;
   if (!Aq || !A_scale || !W13 || !W13_scale || !sorted_ids || !expert_ids || !ntpp || !hq || !hs)
     return kErrNullPointer;
@@ -1226,9 +1251,10 @@ static int w13_gemm(const void* Aq, const float* A_scale, const void* W13, const
   g.N = 2 * I;
   g.K = H;
   g.I = I;
-  g.max_blocks = (max_padded + BM - 1) / BM;
+  g.max_blocks = (max_padded + (BM >> vshift) - 1) / (BM >> vshift);
   g.n_tiles = I / 128;
   g.bma = BM;
+  g.vshift = vshift;
   g.top_k = top_k;
   g.a_by_pos = 0;
   g.E = E;
